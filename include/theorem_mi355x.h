@@ -1,0 +1,135 @@
+/*
+ * theorem_mi355x.h — C ABI of libtheorem_mi355x.so, the MI355X (gfx950) HIP
+ * implementation of Theorem's four hot kernels.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, sizes and dtype codes (no framework types);
+ *   - launches asynchronously on `stream` (a hipStream_t; NULL = the null
+ *     stream) and never synchronises, allocates or frees device memory;
+ *   - validates its arguments on the host BEFORE any launch and returns a
+ *     negative thm_status for an invalid call (nothing is launched), a positive
+ *     hipError_t if the launch itself failed, and THM_OK (0) otherwise;
+ *   - reads its inputs and writes only its outputs; each output element is
+ *     written by exactly one lane, so results are bitwise deterministic.
+ *
+ * Tensor layouts are dense row-major ("contiguous" in PyTorch terms) exactly
+ * as the reference's Python kernels lay them out:
+ *   conv:     x, out [batch, dim, seqlen]; weight [dim, width]; bias [dim]
+ *   DeltaNet: per-token tensors [B, T, H, D] (D = K or V); gates/beta [B, T, H];
+ *             A [B, T, H, chunk_size]; per-chunk states [B, T/chunk_size, H, K, V].
+ */
+#ifndef THEOREM_MI355X_H
+#define THEOREM_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define THM_ABI_VERSION 1
+
+/* Status codes (negative = rejected on the host before any launch). */
+#define THM_OK 0
+#define THM_ERR_NULL_POINTER (-1) /* a required pointer is NULL                */
+#define THM_ERR_BAD_SHAPE (-2)    /* negative/zero/overflowing size, T % BT     */
+#define THM_ERR_BAD_DTYPE (-3)    /* unknown or unsupported dtype code          */
+#define THM_ERR_UNSUPPORTED (-4)  /* valid but not implemented (K, V, width)    */
+#define THM_ERR_MISALIGNED (-5)   /* pointer not aligned to its element size    */
+#define THM_ERR_BAD_ARGUMENT (-6) /* flag/activation/chunk_size out of range    */
+
+/* Element type codes. */
+#define THM_DTYPE_F32 0
+#define THM_DTYPE_BF16 1
+
+/* Activation codes for thm_causal_conv1d_fwd. */
+#define THM_ACT_NONE 0 /* the reference's behaviour (no activation)          */
+#define THM_ACT_SILU 1 /* x * sigmoid(x); extension, not in the reference    */
+
+/* Flags for thm_chunk_fwd_h. */
+#define THM_H_DELTA 1 /* delta-rule form: v_new = u - w.S, h[c] stored BEFORE the
+                         update of chunk c, optional v_new / final-state output.
+                         Without it: the reference's form (v used as is, h[c]
+                         stored AFTER the update of chunk c). */
+
+/* Library ABI version (THM_ABI_VERSION of the build). */
+int thm_abi_version(void);
+
+/* Human-readable text for a status code (static storage, never NULL). */
+const char* thm_status_string(int status);
+
+/*
+ * Depthwise causal 1-D convolution.
+ *   out[b,d,t] = act( bias[d] + sum_{k<width} weight[d,k] * x[b,d,t-width+1+k] ),
+ *   x[b,d,t<0] = 0, fp32 accumulation.
+ * Replaces the launcher `custom_kernel((x, weight, bias))` of
+ * kernels/causal_conv1d/kernel.py:170-230 and its Triton kernel
+ * `causal_conv1d_kernel` (kernel.py:44-117); math of reference.py:55-81.
+ *   x_dtype: dtype of x and out (F32 or BF16); w_dtype: dtype of weight and bias.
+ *   bias may be NULL (treated as zeros; the reference always passes one).
+ *   1 <= width <= 8.
+ */
+int thm_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, void* out,
+                          int64_t batch, int64_t dim, int64_t seqlen, int32_t width,
+                          int32_t x_dtype, int32_t w_dtype, int32_t activation,
+                          void* stream);
+
+/*
+ * Gated DeltaNet WY recompute, per chunk c of chunk_size = 64 tokens:
+ *   w_c = A_c . (k_c * (beta_c * exp(g_c)))      [64 x K]
+ *   u_c = A_c . (v_c * beta_c)                   [64 x V]
+ * with A_c[r, j] = A[b, c*64 + r, h, j] (the full 64x64 block is applied).
+ * Replaces `custom_kernel(Data)` / `_launch` of
+ * kernels/recompute_w_u/kernel.py:192-248 and `recompute_w_u_kernel`
+ * (kernel.py:73-186); math of reference.py:118-149.
+ *   kv_dtype: dtype of k, v, w, u (F32 or BF16). beta, A, g are fp32.
+ *   g may be NULL (no gate: exp(g) = 1).
+ *   K, V in {64, 128}; T % 64 == 0.
+ */
+int thm_recompute_w_u_fwd(const void* k, const void* v, const void* beta, const void* A,
+                          const void* g, void* w, void* u,
+                          int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                          int32_t chunk_size, int32_t kv_dtype, void* stream);
+
+/*
+ * Gated DeltaNet inter-chunk state recurrence over chunks c = 0..T/64-1 of one
+ * (b, head), state S [K x V] fp32 (S = h0 or 0 at c = 0), g_last = g at the
+ * chunk's last token:
+ *   reference form (flags = 0; `vu` = v):
+ *     S <- exp(g_last) S + k_c^T (v_c * exp(g_last - g_c));  h[c] = S
+ *   delta form (flags = THM_H_DELTA; `vu` = u, `w` required):
+ *     h[c] = S;  v_new_c = u_c - w_c . S;
+ *     S <- exp(g_last) S + (k_c * exp(g_last - g_c))^T v_new_c
+ *   ht (optional) receives the final S; v_new (optional, delta form only)
+ *   receives v_new in kv_dtype.
+ * Replaces `custom_kernel(dict)` of kernels/chunk_fwd_h/kernel.py:141-191 and
+ * `chunk_fwd_h_kernel` (kernel.py:61-138); reference form = reference.py:50-97.
+ *   kv_dtype: dtype of k, w, vu, v_new (F32 or BF16). g, h0, h, ht are fp32.
+ *   g may be NULL (no gate). K, V in {64, 128}; T % 64 == 0.
+ */
+int thm_chunk_fwd_h(const void* k, const void* w, const void* vu, const void* g,
+                    const void* h0, void* h, void* v_new, void* ht,
+                    int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                    int32_t chunk_size, int32_t kv_dtype, int32_t flags, void* stream);
+
+/*
+ * Gated DeltaNet chunkwise output, per chunk c and token i of the chunk:
+ *   o[i] = scale * ( sum_{j<=i in chunk} (q_i . k_j) exp(g_i - g_j) v_j
+ *                    + exp(g_i) q_i . h[c] )
+ * (causal mask includes the diagonal). Replaces `custom_kernel(dict)` of
+ * kernels/chunk_fwd_o/kernel.py:146-212 and `_chunk_fwd_o_kernel`
+ * (kernel.py:52-136); math of reference.py:80-142 (there in the equivalent
+ * factored form q*exp(g), v*exp(-g)).
+ *   qkv_dtype: dtype of q, k, v and o (F32 or BF16). g and h are fp32.
+ *   g may be NULL (no gate). K, V in {64, 128}; T % 64 == 0.
+ */
+int thm_chunk_fwd_o(const void* q, const void* k, const void* v, const void* g,
+                    const void* h, void* o, float scale,
+                    int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                    int32_t chunk_size, int32_t qkv_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THEOREM_MI355X_H */

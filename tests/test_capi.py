@@ -1,0 +1,72 @@
+"""CPU-side checks of the C ABI: the library loads, exports every entry point
+declared in include/theorem_mi355x.h, and rejects invalid calls on the host
+(negative status, nothing launched) — no GPU needed."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from theorem_amd.kernels import _capi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "theorem_mi355x.h"
+FAKE = 0x10000  # a non-NULL, 256-byte aligned address that is never dereferenced
+
+
+def declared_symbols() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(thm_\w+)\s*\(", text)))
+
+
+def test_header_lists_entry_points():
+    syms = declared_symbols()
+    assert {"thm_causal_conv1d_fwd", "thm_recompute_w_u_fwd", "thm_chunk_fwd_h",
+            "thm_chunk_fwd_o", "thm_status_string", "thm_abi_version"} <= set(syms)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_capi.LIB_PATH))
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, f"not exported: {missing}"
+    assert set(declared_symbols()) <= set(_capi.SIGNATURES), "ctypes signatures missing"
+
+
+def test_abi_version_and_status_strings():
+    lib = _capi.load_library()
+    assert lib.thm_abi_version() == _capi.ABI_VERSION
+    for code in (0, -1, -2, -3, -4, -5, -6, 1, -99):
+        assert isinstance(_capi.status_string(code), str) and _capi.status_string(code)
+    with pytest.raises(ValueError):
+        _capi.check(-2, "x")
+    with pytest.raises(RuntimeError):
+        _capi.check(1, "x")
+
+
+def conv(**kw):
+    a = dict(x=FAKE, w=FAKE, b=FAKE, out=FAKE, B=1, D=4, S=8, W=4, xd=0, wd=0, act=0)
+    a.update(kw)
+    return _capi.load_library().thm_causal_conv1d_fwd(
+        a["x"], a["w"], a["b"], a["out"], a["B"], a["D"], a["S"], a["W"], a["xd"], a["wd"], a["act"], None)
+
+
+def test_conv_validation():
+    assert conv(x=None) == -1 and conv(w=None) == -1 and conv(out=None) == -1
+    assert conv(D=0) == -2 and conv(B=-1) == -2 and conv(S=-3) == -2
+    assert conv(xd=7) == -3 and conv(wd=2) == -3
+    assert conv(W=0) == -4 and conv(W=9) == -4
+    assert conv(act=5) == -6
+    assert conv(x=FAKE + 2) == -5 and conv(xd=1, x=FAKE + 1) == -5
+    assert conv(B=1 << 40, D=1 << 20) == -2
+    # Empty problems are valid and launch nothing.
+    assert conv(B=0) == 0 and conv(S=0) == 0
+
+
+def test_python_wrapper_rejects_cpu_tensors():
+    from theorem_amd.kernels.causal_conv1d import custom_kernel
+    x = torch.zeros(1, 4, 8)
+    with pytest.raises(AssertionError):
+        custom_kernel((x, torch.zeros(4, 3), torch.zeros(4)))

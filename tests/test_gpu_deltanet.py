@@ -1,0 +1,214 @@
+"""GPU parity of the three Gated DeltaNet kernels (through the drop-in
+custom_kernel wrappers) against the CPU oracle (float64).
+
+Tolerances: rtol = atol = 1e-2 for bf16 inputs (the reference's task.yml
+tolerance and BASELINE.json's bar); fp32 inputs are also held to 1e-3, since
+their products run as bf16 hi/lo splits at ~2^-16 relative accuracy.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import deltanet as odn
+from tests.helpers import assert_close
+from theorem_amd import configs
+from theorem_amd.kernels import chunk_fwd_h, chunk_fwd_o, recompute_w_u
+
+pytestmark = pytest.mark.gpu
+
+TASK_SHAPES = {
+    "recompute_w_u": [(1, 64, 2, 64, 64, 4242), (2, 128, 4, 64, 64, 5236), (1, 256, 4, 64, 128, 1001)],
+    "other": [(1, 64, 1, 64, 64, 4242), (2, 128, 4, 64, 64, 5236), (1, 256, 4, 64, 128, 1001)],
+}
+KV = [(64, 64), (64, 128), (128, 64), (128, 128)]
+
+
+def np_(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+# --------------------------------------------------------------------------- recompute_w_u
+
+@pytest.mark.parametrize("B,T,H,K,V,seed", TASK_SHAPES["recompute_w_u"])
+def test_wu_task_shapes_fp32(dev, B, T, H, K, V, seed):
+    data = recompute_w_u.generate_data(B, T, H, K, V, seed, device="cuda")
+    w, u = recompute_w_u.custom_kernel(data)
+    sync()
+    assert w.dtype == torch.float32 and u.dtype == torch.float32
+    ew, eu = odn.recompute_w_u_ref(*(np_(t) for t in (data.k, data.v, data.beta, data.A, data.g)))
+    assert_close(w, ew, 1e-3, 1e-5, "w")
+    assert_close(u, eu, 1e-3, 1e-5, "u")
+    # The harness reference agrees too (dtype and values).
+    rw, ru = recompute_w_u.ref_kernel(data)
+    assert_close(w, rw, 1e-2, 1e-2, "w vs ref_kernel")
+
+
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_wu_config_inputs(dev, K, V, dtype):
+    d = configs.make_wu_inputs(2, 512, 3, K, V, seed=1, device=dev, dtype=dtype)
+    w, u = recompute_w_u.custom_kernel(recompute_w_u.Data(**d, B=2, T=512, H=3, K=K, V=V))
+    sync()
+    assert w.dtype == dtype
+    ew, eu = odn.recompute_w_u_ref(*(np_(d[n]) for n in ("k", "v", "beta", "A", "g")))
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-3
+    assert_close(w, ew, tol, tol, f"w K={K} V={V} {dtype}")
+    assert_close(u, eu, tol, tol, f"u K={K} V={V} {dtype}")
+
+
+def test_wu_identity_A_and_no_gate(dev):
+    # A = I  =>  w = k beta e^g, u = v beta (closed form); g = None => e^g = 1.
+    d = configs.make_wu_inputs(1, 128, 2, 64, 64, seed=2, device=dev, dtype=torch.float32)
+    eye = torch.eye(64, device=dev).repeat(2, 1).reshape(1, 128, 1, 64).expand(1, 128, 2, 64).contiguous()
+    w, u = recompute_w_u.custom_kernel(recompute_w_u.Data(d["k"], d["v"], d["beta"], eye, d["g"], 1, 128, 2, 64, 64))
+    w0, u0 = recompute_w_u.custom_kernel(recompute_w_u.Data(d["k"], d["v"], d["beta"], eye, None, 1, 128, 2, 64, 64))
+    sync()
+    b = d["beta"].unsqueeze(-1)
+    assert_close(w, d["k"] * b * torch.exp(d["g"]).unsqueeze(-1), 1e-5, 1e-6, "A=I w")
+    assert_close(u, d["v"] * b, 1e-5, 1e-6, "A=I u")
+    assert_close(w0, d["k"] * b, 1e-5, 1e-6, "A=I, g=None w")
+    assert_close(u0, u, 0, 0, "u independent of g")
+
+
+# --------------------------------------------------------------------------- chunk_fwd_o
+
+@pytest.mark.parametrize("B,T,H,K,V,seed", TASK_SHAPES["other"])
+def test_o_task_shapes_fp32(dev, B, T, H, K, V, seed):
+    data = chunk_fwd_o.generate_input(B, T, H, K, V, seed, device="cuda")
+    o = chunk_fwd_o.custom_kernel(data)
+    sync()
+    assert o.dtype == torch.float32 and o.shape == (B, T, H, V)
+    e = odn.chunk_fwd_o_ref(*(np_(data[n]) for n in ("q", "k", "v", "g", "h")), data["scale"])
+    assert_close(o, e, 1e-3, 1e-3, "o")
+    assert_close(o, chunk_fwd_o.ref_kernel(data), 1e-2, 1e-2, "o vs ref_kernel")
+
+
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("gate", ["logsigmoid", "mild"])
+def test_o_config_inputs(dev, K, V, dtype, gate):
+    d = configs.make_o_inputs(2, 512, 3, K, V, seed=3, device=dev, dtype=dtype, gate=gate)
+    o = chunk_fwd_o.custom_kernel(d)
+    sync()
+    assert o.dtype == dtype
+    e = odn.chunk_fwd_o_diff(*(np_(d[n]) for n in ("q", "k", "v", "g", "h")), d["scale"])
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-3
+    assert_close(o, e, tol, tol, f"o K={K} V={V} {dtype} {gate}")
+
+
+def test_o_closed_forms(dev):
+    d = configs.make_o_inputs(1, 128, 2, 64, 64, seed=4, device=dev, dtype=torch.float32)
+    q, k, v, h = d["q"], d["k"], d["v"], d["h"]
+    # h = 0, g = None: o = scale tril_incl(q k^T) v per chunk.
+    o = chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=v, g=None, h=torch.zeros_like(h), scale=0.5))
+    # v = 0: o = scale e^g q h[c].
+    o2 = chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=torch.zeros_like(v), g=d["g"], h=h, scale=0.5))
+    sync()
+    qc = q.double().reshape(1, 2, 64, 2, 64).permute(0, 1, 3, 2, 4)
+    kc = k.double().reshape(1, 2, 64, 2, 64).permute(0, 1, 3, 2, 4)
+    vc = v.double().reshape(1, 2, 64, 2, 64).permute(0, 1, 3, 2, 4)
+    e = 0.5 * (torch.tril(qc @ kc.transpose(-1, -2)) @ vc)
+    assert_close(o, e.permute(0, 1, 3, 2, 4).reshape(1, 128, 2, 64), 1e-4, 1e-4, "h=0,g=0")
+    gc = d["g"].double().reshape(1, 2, 64, 2).permute(0, 1, 3, 2)
+    e2 = 0.5 * (qc * torch.exp(gc).unsqueeze(-1)) @ h.double()
+    assert_close(o2, e2.permute(0, 1, 3, 2, 4).reshape(1, 128, 2, 64), 1e-4, 1e-4, "v=0")
+
+
+# --------------------------------------------------------------------------- chunk_fwd_h
+
+@pytest.mark.parametrize("B,T,H,K,V,seed", TASK_SHAPES["other"])
+def test_h_task_shapes_fp32(dev, B, T, H, K, V, seed):
+    data = chunk_fwd_h.generate_input(B, T, H, K, V, seed, device="cuda:0")
+    h = chunk_fwd_h.custom_kernel(data)
+    sync()
+    assert h.dtype == torch.float32 and h.shape == (B, T // 64, H, K, V)
+    e = odn.chunk_fwd_h_ref(np_(data["k"]), np_(data["v"]), np_(data["g"]))
+    assert_close(h, e, 1e-3, 1e-3, "h")
+    assert_close(h, chunk_fwd_h.ref_kernel(data), 1e-2, 1e-2, "h vs ref_kernel")
+
+
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("gate", ["logsigmoid", "mild", "zero"])
+def test_h_delta_config_inputs(dev, K, V, dtype, gate):
+    T = 1024 if gate != "zero" else 256
+    d = configs.make_h_inputs(2, T, 3, K, V, seed=5, device=dev, dtype=dtype, gate=gate, h0_std=0.1)
+    h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=d["g"],
+                                               initial_state=d["h0"], output_final_state=True))
+    sync()
+    assert h.dtype == torch.float32 and vn.dtype == dtype and ht.dtype == torch.float32
+    eh, evn, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np_(d["w"]), np_(d["u"]), np_(d["g"]), h0=np_(d["h0"]))
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-3
+    assert_close(h, eh, tol, tol, f"h K={K} V={V} {dtype} {gate}")
+    assert_close(vn, evn, tol, tol, f"v_new K={K} V={V} {dtype} {gate}")
+    assert_close(ht, eht, tol, tol, f"final K={K} V={V} {dtype} {gate}")
+
+
+def test_h_delta_cfg3_zero_state(dev):
+    # BASELINE config 3 exactly: B=2, T=1024, H=3, K=V=64, bf16, zero initial state.
+    d = configs.make_h_inputs(2, 1024, 3, 64, 64, seed=0, device=dev)
+    h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=d["g"], output_final_state=True))
+    sync()
+    eh, evn, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np_(d["w"]), np_(d["u"]), np_(d["g"]))
+    assert np.abs(np_(h[:, 0])).max() == 0.0  # h[0] is the (zero) initial state
+    assert_close(h, eh, 1e-2, 1e-2, "h")
+    assert_close(vn, evn, 1e-2, 1e-2, "v_new")
+    assert_close(ht, eht, 1e-2, 1e-2, "final")
+
+
+def test_h_reference_form_extras(dev):
+    # Reference form with initial / final state; w = 0 in the delta form gives the
+    # same states shifted by one chunk (pre- vs post-update storage).
+    d = configs.make_h_inputs(1, 256, 2, 64, 64, seed=6, device=dev, dtype=torch.float32, gate="mild", h0_std=0.2)
+    h_ref, ht_ref = chunk_fwd_h.custom_kernel(dict(k=d["k"], v=d["u"], g=d["g"], initial_state=d["h0"],
+                                                   output_final_state=True))
+    h_del, vn, ht_del = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=torch.zeros_like(d["w"]), u=d["u"], g=d["g"],
+                                                       initial_state=d["h0"], output_final_state=True))
+    sync()
+    assert_close(h_del[:, 1:], h_ref[:, :-1], 1e-5, 1e-5, "shifted states")
+    assert_close(h_del[:, 0], d["h0"], 0, 0, "h[0] = h0")
+    assert_close(ht_del, ht_ref, 1e-5, 1e-5, "final states")
+    assert_close(vn, d["u"], 0, 0, "v_new = u when w = 0")
+    assert_close(ht_ref, h_ref[:, -1], 0, 0, "final = last post-update state")
+
+
+def test_h_empty_sequence_final_state(dev):
+    k = torch.empty(1, 0, 2, 64, device=dev)
+    h0 = torch.randn(1, 2, 64, 64, device=dev)
+    h, ht = chunk_fwd_h.custom_kernel(dict(k=k, v=torch.empty(1, 0, 2, 64, device=dev), g=None,
+                                           initial_state=h0, output_final_state=True))
+    sync()
+    assert h.shape == (1, 0, 2, 64, 64)
+    assert_close(ht, h0, 0, 0, "T=0 final state")
+
+
+# --------------------------------------------------------------------------- full chain
+
+@pytest.mark.parametrize("K,V", [(64, 64), (128, 128)])
+@pytest.mark.parametrize("gate", ["logsigmoid", "mild"])
+def test_chain_matches_token_recurrence(dev, K, V, gate):
+    from theorem_amd.chain import chunk_gated_delta_rule_fwd
+    gen = torch.Generator().manual_seed(11)
+    B, T, H = 1, 256, 2
+    q = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16)
+    k = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16)
+    v = torch.randn(B, T, H, V, generator=gen).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    if gate == "logsigmoid":
+        a = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gen))
+    else:
+        a = -0.05 * torch.rand(B, T, H, generator=gen) - 0.005
+    g = configs.chunk_local_cumsum(a)
+    scale = K ** -0.5
+    o, ht = chunk_gated_delta_rule_fwd(q.to(dev), k.to(dev), v.to(dev), beta.to(dev), g.to(dev), scale,
+                                       output_final_state=True)
+    sync()
+    eo, eS = odn.gated_delta_rule_tokens(np_(q), np_(k), np_(v), np_(beta), np_(a), scale)
+    assert_close(o, eo, 1e-2, 1e-2, f"chain o {gate}")
+    assert_close(ht, eS, 1e-2, 1e-2, f"chain final state {gate}")

@@ -1,0 +1,85 @@
+"""Build libtheorem_mi355x.so (gfx950 HIP kernels + C ABI) in-tree with hipcc.
+
+Usage: python -m theorem_amd.build [-v]
+
+Objects go to theorem_amd/_build/, the shared library to
+theorem_amd/lib/libtheorem_mi355x.so (loaded by theorem_amd.kernels._capi).
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+OBJ_DIR = PKG / "_build"
+LIB_DIR = PKG / "lib"
+LIB_NAME = "libtheorem_mi355x.so"
+LIB_PATH = LIB_DIR / LIB_NAME
+
+SOURCES = [
+    "capi.cpp",
+    "causal_conv1d.hip",
+    "recompute_w_u.hip",
+    "chunk_fwd_h.hip",
+    "chunk_fwd_o.hip",
+]
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# Packed-fp32 VALU ops are disabled for all device code; the host pass warns
+# that it does not know the feature, which is harmless.
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(
+        line for line in (r.stdout + r.stderr).splitlines()
+        if "is not a recognized feature for this target" not in line
+    )
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip() and verbose:
+        print(out)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every source for gfx950 and link the shared library; return its path."""
+    if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    OBJ_DIR.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    srcs = [CSRC / s for s in SOURCES if (CSRC / s).exists()]
+    objs = [OBJ_DIR / (s.name + ".o") for s in srcs]
+    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [
+            ex.submit(_run, [HIPCC, *COMMON_FLAGS, "-c", str(s), "-o", str(o)], verbose)
+            for s, o in zip(srcs, objs)
+        ]
+        for f in futs:
+            f.result()
+    tmp = LIB_DIR / (LIB_NAME + ".tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    p = build(verbose="-v" in sys.argv)
+    print(p)

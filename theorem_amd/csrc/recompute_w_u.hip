@@ -1,0 +1,173 @@
+// Gated DeltaNet WY recompute for MI355X (gfx950):
+//   per chunk c of 64 tokens:  w_c = A_c (k_c * beta_c e^{g_c}),  u_c = A_c (v_c * beta_c)
+//
+// Replaces kernels/recompute_w_u/kernel.py:73-186 (Triton) and its launcher
+// kernel.py:192-248; math of reference.py:118-149.
+//
+// One workgroup (4 wavefronts) per (b, chunk, head) tile:
+//   1. The 64 x (K+V) tile X = [k * beta e^g | v * beta] is scaled in fp32 and
+//      written to LDS as bf16 (plus a bf16 "lo" residual tile for fp32 inputs).
+//   2. Wave wv owns positions t = 16 wv .. 16 wv + 15 and computes the
+//      transposed product  D[n][t] = sum_j X[j][n] A_c[t][j]  with
+//      v_mfma_f32_16x16x32_bf16:  the X^T operand comes from LDS with
+//      ds_read_b64_tr_b16; the A_c^T operand is this wave's 16 rows of A_c,
+//      read once from HBM as fp32 and split into bf16 hi + lo (A enters at
+//      ~fp32 accuracy).  fp32 inputs also split X (hi*hi + hi*lo + lo*hi).
+//   3. The accumulator gives each lane 4 consecutive features of one token,
+//      stored as one 8-byte (bf16) / 16-byte (fp32) write.
+// HBM traffic per tile = k, v, A, beta, g read once + w, u written once.
+#include <type_traits>
+
+#include "mfma.h"
+
+namespace thm {
+namespace {
+
+constexpr int kBT = 64;
+constexpr int kWuThreads = 256;
+
+template <typename IT, int K, int V>
+struct WuCfg {
+  static constexpr bool kSplitX = std::is_same<IT, float>::value;
+  static constexpr int kN = K + V;
+  static constexpr int kPitch = kN + 8;  // LDS row pitch in elements (16-byte pad)
+  static constexpr int kTile = kBT * kPitch;
+  static constexpr int kNB = kN / 16;
+  static constexpr int kVE = 16 / (int)sizeof(IT);  // elements per 16-byte load
+};
+
+template <typename IT, int K, int V>
+__global__ void __launch_bounds__(kWuThreads)
+recompute_w_u_kernel(const IT* __restrict__ k, const IT* __restrict__ v,
+                     const float* __restrict__ beta, const float* __restrict__ A,
+                     const float* __restrict__ g, IT* __restrict__ w, IT* __restrict__ u,
+                     int64_t T, int64_t H, int64_t NT) {
+  using C = WuCfg<IT, K, V>;
+  __shared__ __attribute__((aligned(16))) bf16 xs[(C::kSplitX ? 2 : 1) * C::kTile];
+  bf16* const xhi = xs;
+  bf16* const xlo = xs + (C::kSplitX ? C::kTile : 0);
+
+  // tile -> (b, c, h) with the head fastest: consecutive workgroups read one
+  // contiguous [64 tokens x H x D] block.
+  const int64_t tile = blockIdx.x;
+  const int64_t h = tile % H;
+  const int64_t bc = tile / H;
+  const int64_t c = bc % NT;
+  const int64_t b = bc / NT;
+  const int64_t tok0 = b * T + c * kBT;
+  const int tid = threadIdx.x;
+
+  // 1. Stage X.
+  constexpr int CPR = C::kN / C::kVE;
+  for (int q = tid; q < kBT * CPR; q += kWuThreads) {
+    const int j = q / CPR;
+    const int col = (q - j * CPR) * C::kVE;
+    const int64_t row = (tok0 + j) * H + h;
+    const float bj = beta[row];
+    float sc;
+    const IT* src;
+    if (col < K) {
+      sc = g ? bj * fast_exp(g[row]) : bj;
+      src = k + row * K + col;
+    } else {
+      sc = bj;
+      src = v + row * V + (col - K);
+    }
+    float vals[C::kVE];
+    unpack16(ldg16(src), vals, IT{});
+#pragma unroll
+    for (int i = 0; i < C::kVE; ++i) vals[i] *= sc;
+    bf16* dst = xhi + j * C::kPitch + col;
+    if constexpr (C::kSplitX) {
+      lds_put4(dst, xlo + j * C::kPitch + col, vals, true);
+    } else {
+      *reinterpret_cast<bf16x8*>(dst) = to_bf16x8(vals);
+    }
+  }
+  __syncthreads();
+
+  // 2. D[n][t] = sum_j X[j][n] A_c[t][j] for this wave's 16 positions.
+  const int wv = tid >> 6;
+  const int lane = tid & 63;
+  const int grp = lane >> 4;
+  const int li = lane & 15;
+  const int64_t trow = (tok0 + 16 * wv + li) * H + h;
+  const float* arow = A + trow * kBT;
+  bf16x8 ahi[2], alo[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    float av[8];
+    load8f(arow + 32 * s + 8 * grp, av);
+    split_bf16x8(av, ahi[s], alo[s]);
+  }
+
+#pragma unroll
+  for (int nb = 0; nb < C::kNB; ++nb) {
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int r0 = tr_row_natural(32 * s, 0), r1 = tr_row_natural(32 * s, 1);
+      const bf16x8 xh = frag_tr(xhi, C::kPitch, r0, r1, 16 * nb);
+      acc = mfma16x16x32(xh, ahi[s], acc);
+      acc = mfma16x16x32(xh, alo[s], acc);
+      if constexpr (C::kSplitX) {
+        const bf16x8 xl = frag_tr(xlo, C::kPitch, r0, r1, 16 * nb);
+        acc = mfma16x16x32(xl, ahi[s], acc);
+      }
+    }
+    // 3. Lane holds features n = 16 nb + 4 grp + 0..3 of token t.
+    const int n = 16 * nb + 4 * grp;
+    if (16 * nb < K) {
+      store4(w + trow * K + n, acc);
+    } else {
+      store4(u + trow * V + (n - K), acc);
+    }
+  }
+}
+
+template <typename IT, int K, int V>
+hipError_t launch_wu(const void* k, const void* v, const void* beta, const void* A, const void* g,
+                     void* w, void* u, int64_t B, int64_t T, int64_t H, hipStream_t s) {
+  const int64_t NT = T / kBT;
+  const int64_t tiles = B * NT * H;
+  hipLaunchKernelGGL((recompute_w_u_kernel<IT, K, V>), dim3((unsigned)tiles), dim3(kWuThreads), 0, s,
+                     (const IT*)k, (const IT*)v, (const float*)beta, (const float*)A,
+                     (const float*)g, (IT*)w, (IT*)u, T, H, NT);
+  return hipGetLastError();
+}
+
+template <typename IT>
+hipError_t dispatch_kv(int64_t K, int64_t V, const void* k, const void* v, const void* beta,
+                       const void* A, const void* g, void* w, void* u, int64_t B, int64_t T,
+                       int64_t H, hipStream_t s) {
+  if (K == 64 && V == 64) return launch_wu<IT, 64, 64>(k, v, beta, A, g, w, u, B, T, H, s);
+  if (K == 64 && V == 128) return launch_wu<IT, 64, 128>(k, v, beta, A, g, w, u, B, T, H, s);
+  if (K == 128 && V == 64) return launch_wu<IT, 128, 64>(k, v, beta, A, g, w, u, B, T, H, s);
+  return launch_wu<IT, 128, 128>(k, v, beta, A, g, w, u, B, T, H, s);
+}
+
+}  // namespace
+}  // namespace thm
+
+extern "C" int thm_recompute_w_u_fwd(const void* k, const void* v, const void* beta, const void* A,
+                                     const void* g, void* w, void* u, int64_t B, int64_t T,
+                                     int64_t H, int64_t K, int64_t V, int32_t chunk_size,
+                                     int32_t kv_dtype, void* stream) {
+  using namespace thm;
+  if (chunk_size != kBT) return THM_ERR_BAD_ARGUMENT;
+  if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || T % kBT) return THM_ERR_BAD_SHAPE;
+  if (kv_dtype != THM_DTYPE_F32 && kv_dtype != THM_DTYPE_BF16) return THM_ERR_BAD_DTYPE;
+  if ((K != 64 && K != 128) || (V != 64 && V != 128)) return THM_ERR_UNSUPPORTED;
+  if (B == 0 || T == 0) return THM_OK;  // empty: nothing is read or written
+  if (!k || !v || !beta || !A || !w || !u) return THM_ERR_NULL_POINTER;
+  const void* ptrs[] = {k, v, A, w, u};
+  for (const void* p : ptrs)
+    if ((uintptr_t)p % 16) return THM_ERR_MISALIGNED;
+  if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
+  if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = (kv_dtype == THM_DTYPE_F32)
+                     ? dispatch_kv<float>(K, V, k, v, beta, A, g, w, u, B, T, H, s)
+                     : dispatch_kv<bf16>(K, V, k, v, beta, A, g, w, u, B, T, H, s);
+  return (int)e;
+}
