@@ -1,0 +1,232 @@
+"""Benchmark of the MI355X hot path: one step = causal_conv1d + the Gated
+DeltaNet chunk forward (recompute_w_u -> chunk_fwd_h -> chunk_fwd_o) at
+BASELINE.json config 4 (the largest single-GPU configuration), bf16.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--small]
+
+Prints ONE JSON line (rank 0).  ``value`` is microseconds per step (all four
+kernels, inputs resident in HBM, outputs preallocated by the caching
+allocator).  Per-kernel durations come from HIP events recorded on the stream
+the kernels are launched on (torch's current stream), averaged over the timed
+steps.  ``roofline`` is for the kernel with the largest share of the step:
+algorithmic bytes per launch / its average duration vs 8 TB/s.  ``traffic``
+is read from profiles/traffic_cfg4.json when that summary of rocprofv3
+FETCH_SIZE / WRITE_SIZE runs exists, else null.  ``cpu_baseline`` times the
+CPU oracle on a bounded sample (one batch element of the same workload) and
+scales to a full step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12        # B/s, MI355X published
+MFMA_BF16_PEAK = 2.5e15  # flop/s, dense bf16, MI355X published
+METRIC = "µs/call and % of roofline (HBM GB/s or bf16 MFMA) per kernel, 1×MI355X"
+
+CFG4 = dict(B=8, T=8192, H=16, K=128, V=128)
+CFG4_CONV = dict(B=8, D=4096, S=8192, W=4)
+
+
+# --------------------------------------------------------------------------- algorithmic work
+
+def work_conv(B, D, S, W, eb=2, ebw=2):
+    return 2 * B * D * S * eb + D * (W + 1) * ebw, 2 * W * B * D * S
+
+
+def work_wu(B, T, H, K, V, eb=2):
+    N = B * T * H
+    NC = N // 64
+    return N * (K + V) * eb + N * 8 + N * 64 * 4 + N * (K + V) * eb, NC * 2 * 64 * 64 * (K + V)
+
+
+def work_h(B, T, H, K, V, eb=2, final=True):
+    N = B * T * H
+    NC = N // 64
+    by = N * (2 * K + V) * eb + 4 * N + NC * K * V * 4 + N * V * eb + (B * H * K * V * 4 if final else 0)
+    return by, NC * 4 * 64 * K * V
+
+
+def work_o(B, T, H, K, V, eb=2):
+    N = B * T * H
+    NC = N // 64
+    by = N * (2 * K + V) * eb + 4 * N + NC * K * V * 4 + N * V * eb
+    return by, NC * (2 * 64 * 64 * (K + V) + 2 * 64 * K * V)
+
+
+# --------------------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(torch, inputs, conv_inputs, target_s: float = 12.0):
+    """Time the CPU oracle on a bounded sample of the same workload and scale to a full step.
+
+    One batch element is timed first; the sample then grows to as many batch
+    elements (and repetitions) as fit in about ``target_s`` seconds, and the
+    median per-element time is scaled to the full batch."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import conv as oconv
+    from oracle import deltanet as odn
+
+    n = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(n)
+    Bfull = inputs["q"].shape[0]
+    x, w, bias = conv_inputs
+    wn, bn = w.float().cpu().numpy(), bias.float().cpu().numpy()
+
+    def host(nb):
+        f = lambda t: t[:nb].float().cpu().numpy()  # noqa: E731
+        return tuple(f(inputs[k]) for k in ("q", "k", "v", "beta", "g", "A")) + (x[:nb].float().cpu().numpy(),)
+
+    def run(arrs):
+        q, k, v, beta, g, A, xs = arrs
+        t0 = time.perf_counter()
+        oconv.causal_conv1d_c(xs, wn, bn)
+        t1 = time.perf_counter()
+        ww, uu = odn.recompute_w_u_ref(k, v, beta, A, g, dtype=np.float32)
+        h, vn, _ = odn.chunk_fwd_h_delta(k, ww, uu, g, dtype=np.float32)
+        odn.chunk_fwd_o_diff(q, k, vn, g, h, inputs["scale"], dtype=np.float32)
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    with threadpool_limits(limits=n):
+        one = host(1)
+        # warm-up on a tiny slice (library load, first-touch page faults)
+        oconv.causal_conv1d_c(one[6][:, :8], wn[:8], bn[:8])
+        odn.recompute_w_u_ref(*(a[:, :64, :1] for a in (one[1], one[2], one[3], one[5], one[4])), dtype=np.float32)
+        c1, d1 = run(one)
+        per_elem = c1 + d1
+        nb = int(max(1, min(Bfull, target_s / 3 / max(per_elem, 1e-3))))
+        reps = int(max(1, min(5, target_s / max(per_elem * nb, 1e-3))))
+        arrs = one if nb == 1 else host(nb)
+        times = [run(arrs) for _ in range(reps)]
+    conv_s = sorted(t[0] for t in times)[len(times) // 2] / nb
+    chain_s = sorted(t[1] for t in times)[len(times) // 2] / nb
+    us = (conv_s + chain_s) * Bfull * 1e6
+    return {"value": round(us, 1), "unit": "µs/call", "cores": n, "kind": "port",
+            "sample": (f"oracle/ (C conv single-threaded; NumPy fp32 recompute_w_u/chunk_fwd_h/chunk_fwd_o, "
+                       f"BLAS threads={n}) on batch elements 0..{nb - 1} of config 4, median of {reps} runs, "
+                       f"scaled x{Bfull / nb:g} to the full step; per batch element: conv {1e3 * conv_s:.0f} ms, "
+                       f"chain {1e3 * chain_s:.0f} ms")}
+
+
+# --------------------------------------------------------------------------- main
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--small", action="store_true", help="1/8-size workload (quick check)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the hot-path kernels are single-device; "
+              "multi-GPU sharding is described in DESIGN.md but not launched). Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from theorem_amd import configs
+    from theorem_amd.kernels import causal_conv1d, chunk_fwd_h, chunk_fwd_o, recompute_w_u
+
+    dev = torch.device("cuda:0")
+    shp = dict(CFG4)
+    cshp = dict(CFG4_CONV)
+    if args.small:
+        shp["B"], cshp["B"] = 1, 1
+    t_gen = time.perf_counter()
+    inp = configs.make_chain_inputs(**shp, seed=0, device=dev)
+    conv_in = configs.make_conv_inputs(**cshp, dtype=torch.bfloat16, seed=0, device=dev)
+    torch.cuda.synchronize()
+    print(f"[bench] inputs ready in {time.perf_counter() - t_gen:.1f}s", file=sys.stderr, flush=True)
+
+    B, T, H, K, V = (shp[n] for n in ("B", "T", "H", "K", "V"))
+    q, k, v, beta, g, A, scale = (inp[n] for n in ("q", "k", "v", "beta", "g", "A", "scale"))
+    names = ["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o"]
+
+    def step(ev=None):
+        def mark(i):
+            if ev is not None:
+                ev[i].record()
+        mark(0)
+        y = causal_conv1d.custom_kernel(conv_in)
+        mark(1)
+        w, u = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V))
+        mark(2)
+        h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=k, w=w, u=u, g=g, output_final_state=True))
+        mark(3)
+        o = chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=vn, g=g, h=h, scale=scale))
+        mark(4)
+        return y, o, ht
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    per = {n: sum(e[j].elapsed_time(e[j + 1]) for e in evs) * 1e3 / args.steps for j, n in enumerate(names)}
+
+    works = {
+        "causal_conv1d": work_conv(**cshp),
+        "recompute_w_u": work_wu(B, T, H, K, V),
+        "chunk_fwd_h": work_h(B, T, H, K, V),
+        "chunk_fwd_o": work_o(B, T, H, K, V),
+    }
+    kernels = {}
+    for n in names:
+        by, fl = works[n]
+        us = per[n]
+        kernels[n] = {"us": round(us, 2), "bytes": by, "flops": fl,
+                      "GBps": round(by / us / 1e3, 1), "TFLOPs": round(fl / us / 1e6, 2),
+                      "hbm_frac": round(by / (us * 1e-6) / HBM_PEAK, 4),
+                      "mfma_frac": round(fl / (us * 1e-6) / MFMA_BF16_PEAK, 4)}
+    dom = max(names, key=lambda n: per[n])
+    traffic = None
+    tpath = ROOT / "profiles" / "traffic_cfg4.json"
+    if tpath.exists() and not args.small:
+        try:
+            traffic = json.loads(tpath.read_text()).get(dom, {}).get("hbm_bytes_per_launch")
+        except Exception:  # noqa: BLE001
+            traffic = None
+    by, _ = works[dom]
+    achieved = by / (per[dom] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
+                "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic}
+
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(torch, inp, conv_in)
+
+    workload = (f"cfg4: causal_conv1d ({cshp['B']},{cshp['D']},{cshp['S']},W={cshp['W']}) bf16 + Gated DeltaNet "
+                f"chunk fwd recompute_w_u->chunk_fwd_h->chunk_fwd_o B={B},T={T},H={H},K={K},V={V},BT=64 bf16")
+    line = {
+        "metric": METRIC, "value": round(ms_per_step * 1e3, 2), "unit": "µs/call", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded torch CPU generator; BASELINE.json config-4 distributions)",
+        "config": {"workload": workload, "parallelism": "single GPU"},
+        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
