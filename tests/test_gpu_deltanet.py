@@ -70,9 +70,10 @@ def test_wu_identity_A_and_no_gate(dev):
     w0, u0 = recompute_w_u.custom_kernel(recompute_w_u.Data(d["k"], d["v"], d["beta"], eye, None, 1, 128, 2, 64, 64))
     sync()
     b = d["beta"].unsqueeze(-1)
-    assert_close(w, d["k"] * b * torch.exp(d["g"]).unsqueeze(-1), 1e-5, 1e-6, "A=I w")
-    assert_close(u, d["v"] * b, 1e-5, 1e-6, "A=I u")
-    assert_close(w0, d["k"] * b, 1e-5, 1e-6, "A=I, g=None w")
+    # fp32 operands run as bf16 hi/lo splits (~2^-16 relative per product).
+    assert_close(w, d["k"] * b * torch.exp(d["g"]).unsqueeze(-1), 1e-4, 1e-6, "A=I w")
+    assert_close(u, d["v"] * b, 1e-4, 1e-6, "A=I u")
+    assert_close(w0, d["k"] * b, 1e-4, 1e-6, "A=I, g=None w")
     assert_close(u0, u, 0, 0, "u independent of g")
 
 

@@ -202,18 +202,9 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
       S[kb][r] = h0 ? h0[(bh * K + 16 * kb + 4 * grp + r) * V + vcol] : 0.f;
   }
 
-  u32x4 pf[C::kPer];
-  if (NT > 0) {
-    h_prefetch<IT, K, BV, DELTA>(pf, k, w, vu, g, b * T, H, hh, V, v0);
-    h_commit<IT, K, BV, DELTA>(pf, stage(0));
-    __syncthreads();
-  }
-
-  for (int64_t c = 0; c < NT; ++c) {
-    const St cs = stage((int)(c % C::kStages));
+  // One chunk of work on the tiles staged in `cs`.
+  auto chunk = [&](const St& cs, int64_t c) {
     const int64_t tok0 = b * T + c * kBT;
-    if (c + 1 < NT) h_prefetch<IT, K, BV, DELTA>(pf, k, w, vu, g, tok0 + kBT, H, hh, V, v0);
-
     float* hc = hout + ((b * NT + c) * H + hh) * (int64_t)K * V;
     if constexpr (DELTA) {
 #pragma unroll
@@ -302,6 +293,19 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
         for (int r = 0; r < 4; ++r) hc[(16 * kb + 4 * grp + r) * V + vcol] = S[kb][r];
     }
 
+  };
+
+  // The next chunk's loads are issued before the current chunk computes and
+  // written to the other LDS stage after it.
+  u32x4 pf[C::kPer];
+  if (NT > 0) {
+    h_prefetch<IT, K, BV, DELTA>(pf, k, w, vu, g, b * T, H, hh, V, v0);
+    h_commit<IT, K, BV, DELTA>(pf, stage(0));
+    __syncthreads();
+  }
+  for (int64_t c = 0; c < NT; ++c) {
+    if (c + 1 < NT) h_prefetch<IT, K, BV, DELTA>(pf, k, w, vu, g, b * T + (c + 1) * kBT, H, hh, V, v0);
+    chunk(stage((int)(c % C::kStages)), c);
     if (c + 1 < NT) {
       if constexpr (C::kStages == 1) __syncthreads();  // every wave is done with the stage
       h_commit<IT, K, BV, DELTA>(pf, stage((int)((c + 1) % C::kStages)));

@@ -6,12 +6,15 @@
 // factored gates q e^{g}, v e^{-g}.  Here only e^{g_i - g_j} with j <= i is
 // formed, which cannot overflow for a non-increasing gate.
 //
-// One workgroup (4 wavefronts) per (b, chunk, head) tile.  v_c [64 x V] and
-// h[c] [K x V] are staged in LDS as bf16 (fp32 inputs: bf16 hi + lo).  Wave wv
-// owns query positions i = 16 wv .. 16 wv + 15 and computes o^T (features x
-// positions), so each lane ends with 4 consecutive features of one token:
+// One workgroup (4 wavefronts) per (b, chunk, head) tile, one memory phase:
+// every global load of the tile (v_c, h[c], this wave's q rows and the k rows
+// of its key blocks, g) is issued before the first wait.  v_c [64 x V] and
+// h[c] [K x V] are then staged in LDS as bf16 (fp32 inputs: bf16 hi + lo).
+// Wave wv owns query positions i = 16 wv .. 16 wv + 15 and computes o^T
+// (features x positions), so each lane ends with 4 consecutive features of
+// one token:
 //   1. acc[n][i]  = sum_kappa h[kappa][n] q[i][kappa]          (h^T from LDS via
-//      ds_read_b64_tr_b16, q straight from HBM), then acc *= e^{g_i};
+//      ds_read_b64_tr_b16, q fragments from registers), then acc *= e^{g_i};
 //   2. S^T[j][i]  = sum_kappa k[j][kappa] q[i][kappa] for key blocks j <= i;
 //      P[i][j] = S^T[j][i] e^{g_i - g_j} (0 for j > i), kept in registers;
 //   3. acc[n][i] += sum_j v[j][n] P[i][j]: the P accumulator pairs are the B
@@ -35,7 +38,39 @@ struct OCfg {
   static constexpr int kHTile = K * kPitch;
   static constexpr int kLds = (kSplit ? 2 : 1) * (kVTile + kHTile);
   static constexpr int kVE = 16 / (int)sizeof(IT);
+  static constexpr int kVCPR = V / kVE;                         // 16-byte chunks per v row
+  static constexpr int kVLoads = kBT * kVCPR / kOThreads;
+  static constexpr int kHLoads = K * (V / 4) / kOThreads;       // h is fp32
+  static constexpr int KS = K / 32;                             // contraction steps over K
+  static constexpr int kFragLoads = kSplit ? 2 : 1;             // 16-byte loads per 8-element fragment
+  static_assert(kBT * kVCPR % kOThreads == 0 && K * (V / 4) % kOThreads == 0, "staging split");
 };
+
+// 8 elements of a q / k row as an MFMA fragment (fp32: raw, split at use).
+template <typename IT>
+struct RowFrag {
+  u32x4 r[sizeof(IT) == 4 ? 2 : 1];
+};
+
+template <typename IT>
+__device__ __forceinline__ RowFrag<IT> load_frag(const IT* p) {
+  RowFrag<IT> f;
+  f.r[0] = ldg16(p);
+  if constexpr (sizeof(IT) == 4) f.r[1] = ldg16(p + 4);
+  return f;
+}
+
+template <typename IT>
+__device__ __forceinline__ void frag_bf16(const RowFrag<IT>& f, bf16x8& hi, bf16x8& lo) {
+  if constexpr (sizeof(IT) == 4) {
+    float v[8];
+    unpack16(f.r[0], v, 0.f);
+    unpack16(f.r[1], v + 4, 0.f);
+    split_bf16x8(v, hi, lo);
+  } else {
+    hi = __builtin_bit_cast(bf16x8, f.r[0]);
+  }
+}
 
 template <typename IT, int K, int V>
 __global__ void __launch_bounds__(kOThreads)
@@ -43,6 +78,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
                    const float* __restrict__ g, const float* __restrict__ hs, IT* __restrict__ o,
                    float scale, int64_t T, int64_t H, int64_t NT) {
   using C = OCfg<IT, K, V>;
+  constexpr int KS = C::KS;
   __shared__ __attribute__((aligned(16))) bf16 lds[C::kLds];
   __shared__ float gs[kBT];
   bf16* const vhi = lds;
@@ -57,34 +93,6 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
   const int64_t b = bc / NT;
   const int64_t tok0 = b * T + c * kBT;
   const int tid = threadIdx.x;
-
-  // Stage v_c (IT) and h[c] (fp32) as bf16 (hi[, lo]).
-  {
-    constexpr int VCPR = V / C::kVE;
-    for (int qi = tid; qi < kBT * VCPR; qi += kOThreads) {
-      const int j = qi / VCPR;
-      const int col = (qi - j * VCPR) * C::kVE;
-      float vals[C::kVE];
-      unpack16(ldg16(v + ((tok0 + j) * H + hh) * V + col), vals, IT{});
-      if constexpr (C::kSplit) {
-        lds_put4(vhi + j * C::kPitch + col, vlo + j * C::kPitch + col, vals, true);
-      } else {
-        *reinterpret_cast<bf16x8*>(vhi + j * C::kPitch + col) = to_bf16x8(vals);
-      }
-    }
-    const float* hsrc = hs + ((b * NT + c) * H + hh) * (int64_t)(K * V);
-    constexpr int HCPR = V / 4;
-    for (int qi = tid; qi < K * HCPR; qi += kOThreads) {
-      const int r = qi / HCPR;
-      const int col = (qi - r * HCPR) * 4;
-      float vals[4];
-      unpack16(ldg16(hsrc + r * V + col), vals, 0.f);
-      lds_put4(hhi + r * C::kPitch + col, hlo + r * C::kPitch + col, vals, C::kSplit);
-    }
-    if (tid < kBT) gs[tid] = g ? g[(tok0 + tid) * H + hh] : 0.f;
-  }
-  __syncthreads();
-
   const int wv = tid >> 6;
   const int lane = tid & 63;
   const int grp = lane >> 4;
@@ -92,21 +100,67 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
   const int i = 16 * wv + li;  // this lane's query position (column of every accumulator)
   const int64_t qrow = (tok0 + i) * H + hh;
 
-  // q fragments, natural contraction order: q[i][32 s + 8 grp + 0..7].
-  constexpr int KS = K / 32;
-  bf16x8 qh[KS], ql[KS];
+  // 1. Issue every global load of the tile.
+  u32x4 vr[C::kVLoads], hr[C::kHLoads];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
+  for (int it = 0; it < C::kVLoads; ++it) {
+    const int qi = tid + it * kOThreads;
+    const int j = qi / C::kVCPR;
+    const int col = (qi - j * C::kVCPR) * C::kVE;
+    vr[it] = ldg16(v + ((tok0 + j) * H + hh) * V + col);
+  }
+  const float* hsrc = hs + ((b * NT + c) * H + hh) * (int64_t)(K * V);
+#pragma unroll
+  for (int it = 0; it < C::kHLoads; ++it) {
+    const int qi = tid + it * kOThreads;
+    const int r = qi / (V / 4);
+    const int col = (qi - r * (V / 4)) * 4;
+    hr[it] = ldg16(hsrc + r * V + col);
+  }
+  // q fragments q[i][32 s + 8 grp + 0..7] and k fragments of key blocks jb <= wv.
+  RowFrag<IT> qf[KS], kf[4][KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qf[s] = load_frag(q + qrow * K + 32 * s + 8 * grp);
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    if (jb > wv) continue;  // wave-uniform
+    const int64_t krow = (tok0 + 16 * jb + li) * H + hh;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kf[jb][s] = load_frag(k + krow * K + 32 * s + 8 * grp);
+  }
+  const float gload = (tid < kBT && g) ? g[(tok0 + tid) * H + hh] : 0.f;
+
+  // 2. Stage v_c and h[c] as bf16 (hi[, lo]) and g.
+#pragma unroll
+  for (int it = 0; it < C::kVLoads; ++it) {
+    const int qi = tid + it * kOThreads;
+    const int j = qi / C::kVCPR;
+    const int col = (qi - j * C::kVCPR) * C::kVE;
     if constexpr (C::kSplit) {
-      float f[8];
-      load8f(q + qrow * K + 32 * s + 8 * grp, f);
-      split_bf16x8(f, qh[s], ql[s]);
+      float vals[4];
+      unpack16(vr[it], vals, 0.f);
+      lds_put4(vhi + j * C::kPitch + col, vlo + j * C::kPitch + col, vals, true);
     } else {
-      qh[s] = load8(reinterpret_cast<const bf16*>(q) + qrow * K + 32 * s + 8 * grp);
+      *reinterpret_cast<u32x4*>(vhi + j * C::kPitch + col) = vr[it];
     }
   }
+#pragma unroll
+  for (int it = 0; it < C::kHLoads; ++it) {
+    const int qi = tid + it * kOThreads;
+    const int r = qi / (V / 4);
+    const int col = (qi - r * (V / 4)) * 4;
+    float vals[4];
+    unpack16(hr[it], vals, 0.f);
+    lds_put4(hhi + r * C::kPitch + col, hlo + r * C::kPitch + col, vals, C::kSplit);
+  }
+  if (tid < kBT) gs[tid] = gload;
+  __syncthreads();
 
-  // 1. Inter-chunk term.
+  bf16x8 qh[KS], ql[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) frag_bf16(qf[s], qh[s], ql[s]);
+
+  // 3. Inter-chunk term, then scaled by e^{g_i}.
   constexpr int NB = V / 16;
   f32x4 acc[NB];
 #pragma unroll
@@ -129,26 +183,20 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] *= egi;
 
-  // 2. Gated, causally masked scores for key blocks jb <= wv.
+  // 4. Gated, causally masked scores S^T[j][i] for key blocks jb <= wv.
   f32x4 p[4];
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) {
     p[jb] = zero4();
     if (jb > wv) continue;  // wave-uniform
-    const int64_t krow = (tok0 + 16 * jb + li) * H + hh;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
+      bf16x8 kh, kl;
+      frag_bf16(kf[jb][s], kh, kl);
+      p[jb] = mfma16x16x32(kh, qh[s], p[jb]);
       if constexpr (C::kSplit) {
-        float f[8];
-        bf16x8 kh, kl;
-        load8f(k + krow * K + 32 * s + 8 * grp, f);
-        split_bf16x8(f, kh, kl);
-        p[jb] = mfma16x16x32(kh, qh[s], p[jb]);
         p[jb] = mfma16x16x32(kh, ql[s], p[jb]);
         p[jb] = mfma16x16x32(kl, qh[s], p[jb]);
-      } else {
-        const bf16x8 kf = load8(reinterpret_cast<const bf16*>(k) + krow * K + 32 * s + 8 * grp);
-        p[jb] = mfma16x16x32(kf, qh[s], p[jb]);
       }
     }
     // lane holds S^T[j = 16 jb + 4 grp + r][i]
@@ -159,7 +207,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     }
   }
 
-  // 3. Intra-chunk term: key steps of 32 (block pairs 2s, 2s+1).
+  // 5. Intra-chunk term: key steps of 32 (block pairs 2s, 2s+1), paired order.
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     if (2 * s > wv) continue;  // wave-uniform: both blocks fully masked
@@ -184,7 +232,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     }
   }
 
-  // 4. o[i][16 nb + 4 grp + 0..3].
+  // 6. o[i][16 nb + 4 grp + 0..3].
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) store4(o + qrow * V + 16 * nb + 4 * grp, acc[nb] * scale);
 }

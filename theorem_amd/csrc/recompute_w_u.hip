@@ -4,17 +4,21 @@
 // Replaces kernels/recompute_w_u/kernel.py:73-186 (Triton) and its launcher
 // kernel.py:192-248; math of reference.py:118-149.
 //
-// One workgroup (4 wavefronts) per (b, chunk, head) tile:
-//   1. The 64 x (K+V) tile X = [k * beta e^g | v * beta] is scaled in fp32 and
-//      written to LDS as bf16 (plus a bf16 "lo" residual tile for fp32 inputs).
-//   2. Wave wv owns positions t = 16 wv .. 16 wv + 15 and computes the
-//      transposed product  D[n][t] = sum_j X[j][n] A_c[t][j]  with
-//      v_mfma_f32_16x16x32_bf16:  the X^T operand comes from LDS with
-//      ds_read_b64_tr_b16; the A_c^T operand is this wave's 16 rows of A_c,
-//      read once from HBM as fp32 and split into bf16 hi + lo (A enters at
-//      ~fp32 accuracy).  fp32 inputs also split X (hi*hi + hi*lo + lo*hi).
-//   3. The accumulator gives each lane 4 consecutive features of one token,
-//      stored as one 8-byte (bf16) / 16-byte (fp32) write.
+// One workgroup (4 wavefronts) per (b, chunk, head) tile, one memory phase:
+//   1. Every global load of the tile is issued at once: the 64 x (K+V) tile
+//      X = [k | v] (16-byte loads into registers), this wave's 16 rows of A_c
+//      (fp32), and beta / g.
+//   2. X goes to LDS unchanged for bf16 inputs (fp32 inputs: bf16 hi + lo);
+//      beta, g go to LDS; one barrier.
+//   3. The per-token scales are folded into A instead of X:
+//        w = (A diag(beta e^g)) k,   u = (A diag(beta)) v,
+//      each scaled A operand split into bf16 hi + lo (so A, beta and e^g enter
+//      at ~fp32 accuracy and bf16 k / v enter exactly).
+//   4. Wave wv owns positions t = 16 wv .. 16 wv + 15 and computes the
+//      transposed product D[n][t] = sum_j X[j][n] A'[t][j] with
+//      v_mfma_f32_16x16x32_bf16; X^T is read from LDS with ds_read_b64_tr_b16.
+//      Each lane ends with 4 consecutive features of one token: one 8-byte
+//      (bf16) / 16-byte (fp32) store.
 // HBM traffic per tile = k, v, A, beta, g read once + w, u written once.
 #include <type_traits>
 
@@ -30,10 +34,13 @@ template <typename IT, int K, int V>
 struct WuCfg {
   static constexpr bool kSplitX = std::is_same<IT, float>::value;
   static constexpr int kN = K + V;
-  static constexpr int kPitch = kN + 8;  // LDS row pitch in elements (16-byte pad)
+  static constexpr int kPitch = kN + 8;  // LDS row pitch in bf16 elements (16-byte pad)
   static constexpr int kTile = kBT * kPitch;
   static constexpr int kNB = kN / 16;
   static constexpr int kVE = 16 / (int)sizeof(IT);  // elements per 16-byte load
+  static constexpr int kCPR = kN / kVE;             // 16-byte chunks per row
+  static constexpr int kLoads = kBT * kCPR / kWuThreads;
+  static_assert(kBT * kCPR % kWuThreads == 0, "staging must divide evenly");
 };
 
 template <typename IT, int K, int V>
@@ -44,6 +51,7 @@ recompute_w_u_kernel(const IT* __restrict__ k, const IT* __restrict__ v,
                      int64_t T, int64_t H, int64_t NT) {
   using C = WuCfg<IT, K, V>;
   __shared__ __attribute__((aligned(16))) bf16 xs[(C::kSplitX ? 2 : 1) * C::kTile];
+  __shared__ float sbeta[kBT], sg[kBT];
   bf16* const xhi = xs;
   bf16* const xlo = xs + (C::kSplitX ? C::kTile : 0);
 
@@ -56,68 +64,87 @@ recompute_w_u_kernel(const IT* __restrict__ k, const IT* __restrict__ v,
   const int64_t b = bc / NT;
   const int64_t tok0 = b * T + c * kBT;
   const int tid = threadIdx.x;
-
-  // 1. Stage X.
-  constexpr int CPR = C::kN / C::kVE;
-  for (int q = tid; q < kBT * CPR; q += kWuThreads) {
-    const int j = q / CPR;
-    const int col = (q - j * CPR) * C::kVE;
-    const int64_t row = (tok0 + j) * H + h;
-    const float bj = beta[row];
-    float sc;
-    const IT* src;
-    if (col < K) {
-      sc = g ? bj * fast_exp(g[row]) : bj;
-      src = k + row * K + col;
-    } else {
-      sc = bj;
-      src = v + row * V + (col - K);
-    }
-    float vals[C::kVE];
-    unpack16(ldg16(src), vals, IT{});
-#pragma unroll
-    for (int i = 0; i < C::kVE; ++i) vals[i] *= sc;
-    bf16* dst = xhi + j * C::kPitch + col;
-    if constexpr (C::kSplitX) {
-      lds_put4(dst, xlo + j * C::kPitch + col, vals, true);
-    } else {
-      *reinterpret_cast<bf16x8*>(dst) = to_bf16x8(vals);
-    }
-  }
-  __syncthreads();
-
-  // 2. D[n][t] = sum_j X[j][n] A_c[t][j] for this wave's 16 positions.
   const int wv = tid >> 6;
   const int lane = tid & 63;
   const int grp = lane >> 4;
   const int li = lane & 15;
+
+  // 1. Issue every load.
+  u32x4 xr[C::kLoads];
+#pragma unroll
+  for (int it = 0; it < C::kLoads; ++it) {
+    const int q = tid + it * kWuThreads;
+    const int j = q / C::kCPR;
+    const int col = (q - j * C::kCPR) * C::kVE;
+    const int64_t row = (tok0 + j) * H + h;
+    xr[it] = ldg16(col < K ? (const void*)(k + row * K + col) : (const void*)(v + row * V + (col - K)));
+  }
   const int64_t trow = (tok0 + 16 * wv + li) * H + h;
   const float* arow = A + trow * kBT;
-  bf16x8 ahi[2], alo[2];
+  float av[2][8];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    float av[8];
-    load8f(arow + 32 * s + 8 * grp, av);
-    split_bf16x8(av, ahi[s], alo[s]);
+  for (int s = 0; s < 2; ++s) load8f(arow + 32 * s + 8 * grp, av[s]);
+  float bj = 0.f, gj = 0.f;
+  if (tid < kBT) {
+    const int64_t row = (tok0 + tid) * H + h;
+    bj = beta[row];
+    gj = g ? g[row] : 0.f;
   }
 
+  // 2. Stage X, beta, g.
+#pragma unroll
+  for (int it = 0; it < C::kLoads; ++it) {
+    const int q = tid + it * kWuThreads;
+    const int j = q / C::kCPR;
+    const int col = (q - j * C::kCPR) * C::kVE;
+    if constexpr (C::kSplitX) {
+      float vals[4];
+      unpack16(xr[it], vals, 0.f);
+      lds_put4(xhi + j * C::kPitch + col, xlo + j * C::kPitch + col, vals, true);
+    } else {
+      *reinterpret_cast<u32x4*>(xhi + j * C::kPitch + col) = xr[it];
+    }
+  }
+  if (tid < kBT) {
+    sbeta[tid] = bj;
+    sg[tid] = gj;
+  }
+  __syncthreads();
+
+  // 3. Scaled A operands: A'[t][j] for j = 32 s + 8 grp + 0..7.
+  bf16x8 awh[2], awl[2], auh[2], aul[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    float fw[8], fu[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = 32 * s + 8 * grp + i;
+      const float bb = sbeta[j];
+      fu[i] = av[s][i] * bb;
+      fw[i] = fu[i] * fast_exp(sg[j]);
+    }
+    split_bf16x8(fw, awh[s], awl[s]);
+    split_bf16x8(fu, auh[s], aul[s]);
+  }
+
+  // 4. D[n][t] = sum_j X[j][n] A'[t][j].
 #pragma unroll
   for (int nb = 0; nb < C::kNB; ++nb) {
+    const bool is_w = 16 * nb < K;
     f32x4 acc = zero4();
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int r0 = tr_row_natural(32 * s, 0), r1 = tr_row_natural(32 * s, 1);
       const bf16x8 xh = frag_tr(xhi, C::kPitch, r0, r1, 16 * nb);
-      acc = mfma16x16x32(xh, ahi[s], acc);
-      acc = mfma16x16x32(xh, alo[s], acc);
+      acc = mfma16x16x32(xh, is_w ? awh[s] : auh[s], acc);
+      acc = mfma16x16x32(xh, is_w ? awl[s] : aul[s], acc);
       if constexpr (C::kSplitX) {
         const bf16x8 xl = frag_tr(xlo, C::kPitch, r0, r1, 16 * nb);
-        acc = mfma16x16x32(xl, ahi[s], acc);
+        acc = mfma16x16x32(xl, is_w ? awh[s] : auh[s], acc);
       }
     }
-    // 3. Lane holds features n = 16 nb + 4 grp + 0..3 of token t.
     const int n = 16 * nb + 4 * grp;
-    if (16 * nb < K) {
+    if (is_w) {
       store4(w + trow * K + n, acc);
     } else {
       store4(u + trow * V + (n - K), acc);
