@@ -9,8 +9,8 @@
 // Replaces kernels/chunk_fwd_h/kernel.py:61-138 (Triton) and its launcher
 // kernel.py:141-191.
 //
-// One workgroup per (b, head, V-tile of BV columns), BV / 16 wavefronts; wave
-// wv owns state columns 16 wv .. 16 wv + 15 of the tile for the whole sequence,
+// One workgroup per (b, head, V-tile of 64 columns), 4 wavefronts; wave wv
+// owns state columns 16 wv .. 16 wv + 15 of the tile for the whole sequence,
 // held in MFMA accumulators (K/16 tiles of 16x16 fp32).  Per chunk:
 //   P1 (delta)  v_new^[j][n] = sum_kappa w[j][kappa] S[kappa][n]: the S
 //               accumulator pairs are the B operand in paired order, w rows
@@ -20,7 +20,9 @@
 //               operand, k^T comes from LDS with ds_read_b64_tr_b16.
 // The next chunk's k, w, u/v and g are loaded into registers while the
 // current chunk computes, then written to the other half of a double-buffered
-// LDS stage: the only serial dependency is the state itself.
+// LDS stage: the only serial dependency is the state itself.  Every address
+// in the chunk loop is a wave-uniform chunk base plus a per-lane 32-bit offset
+// fixed before the loop, so the loop spends no VALU on address arithmetic.
 // Workgroups map XCD-aware: the V-tiles of one (b, head) share an XCD (and its
 // L2), so k and w are fetched from HBM once per (b, head).
 #include <type_traits>
@@ -31,36 +33,36 @@ namespace thm {
 namespace {
 
 constexpr int kBT = 64;
+constexpr int kHBV = 64;        // V-tile width
+constexpr int kHThreads = 256;  // 4 wavefronts x 16 state columns
 
-template <typename IT, int K, int BV, bool DELTA>
+template <typename IT, int K, int V, bool DELTA>
 struct HCfg {
   static constexpr bool kSplit = std::is_same<IT, float>::value;
-  static constexpr int kWaves = BV / 16;
-  static constexpr int kThreads = kWaves * 64;
-  static constexpr int kVE = 16 / (int)sizeof(IT);   // elements per 16-byte load
-  static constexpr int kKPitch = K + 8;              // bf16 elements
-  static constexpr int kUPitch = BV + 16 / (int)sizeof(IT);
+  static constexpr int kEB = (int)sizeof(IT);
+  static constexpr int kVE = 16 / kEB;               // elements per 16-byte load
+  static constexpr int kKPitch = K + 8;              // bf16 elements (16-byte pad)
+  static constexpr int kUPitch = kHBV + kVE;         // IT elements (16-byte pad)
   static constexpr int kKTile = kBT * kKPitch;       // bf16 elements
   static constexpr int kUTile = kBT * kUPitch;       // IT elements
   // bf16 elements of one stage: k (hi[, lo]), w (hi[, lo]) when DELTA
   static constexpr int kBf16PerStage = (kSplit ? 2 : 1) * (DELTA ? 2 : 1) * kKTile;
-  // 16-byte chunks of one chunk's inputs
-  static constexpr int kKChunks = kBT * K / kVE;
-  static constexpr int kWChunks = DELTA ? kKChunks : 0;
-  static constexpr int kUChunks = kBT * BV / kVE;
-  static constexpr int kGChunks = kBT / 4;
-  static constexpr int kChunks = kKChunks + kWChunks + kUChunks + kGChunks;
-  static constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+  // per-thread 16-byte load slots of one chunk
+  static constexpr int kKCPR = K / kVE;              // 16-byte chunks per k / w row
+  static constexpr int kKLoads = kBT * kKCPR / kHThreads;
+  static constexpr int kUCPR = kHBV / kVE;           // 16-byte chunks per u row of the tile
+  static constexpr int kULoads = kBT * kUCPR / kHThreads;
+  static_assert(kHThreads % kKCPR == 0 && kHThreads % kUCPR == 0, "slot mapping");
+  static_assert(kBT * kKCPR % kHThreads == 0 && kBT * kUCPR % kHThreads == 0, "slot count");
   static constexpr int kStageBytes =
-      kBf16PerStage * 2 + kUTile * (int)sizeof(IT) + kBT * (int)sizeof(float);
+      kBf16PerStage * 2 + kUTile * kEB + kBT * (int)sizeof(float);
   // Double-buffer the stage when two fit in 128 KiB of LDS; otherwise one stage
   // (fp32 inputs with K = 128) and a barrier before it is overwritten.
   static constexpr int kStages = (2 * kStageBytes <= 128 * 1024) ? 2 : 1;
 };
 
-template <typename IT, int K, int BV, bool DELTA>
+template <typename IT>
 struct HStage {
-  using C = HCfg<IT, K, BV, DELTA>;
   bf16* khi;
   bf16* klo;
   bf16* whi;
@@ -69,89 +71,32 @@ struct HStage {
   float* g;
 };
 
-template <typename IT, int K, int BV, bool DELTA>
-__device__ __forceinline__ void h_prefetch(u32x4* pf, const IT* k,
-                                           const IT* w, const IT* vu, const float* g,
-                                           int64_t tok0, int64_t H, int64_t hh, int64_t V,
-                                           int64_t v0) {
-  using C = HCfg<IT, K, BV, DELTA>;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int it = 0; it < C::kPer; ++it) {
-    const int q = tid + it * C::kThreads;
-    if (q >= C::kChunks) break;
-    if (q < C::kKChunks + C::kWChunks) {
-      const bool isw = q >= C::kKChunks;
-      const int qq = isw ? q - C::kKChunks : q;
-      constexpr int CPR = K / C::kVE;
-      const int j = qq / CPR;
-      const int col = (qq - j * CPR) * C::kVE;
-      const IT* src = (isw ? w : k) + ((tok0 + j) * H + hh) * K + col;
-      pf[it] = ldg16(src);
-    } else if (q < C::kKChunks + C::kWChunks + C::kUChunks) {
-      const int qq = q - C::kKChunks - C::kWChunks;
-      constexpr int CPR = BV / C::kVE;
-      const int j = qq / CPR;
-      const int col = (qq - j * CPR) * C::kVE;
-      pf[it] = ldg16(vu + ((tok0 + j) * H + hh) * V + v0 + col);
-    } else {
-      const int j0 = (q - C::kKChunks - C::kWChunks - C::kUChunks) * 4;
-      if (g) {
-        u32x4 r;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = __float_as_uint(g[(tok0 + j0 + e) * H + hh]);
-        pf[it] = r;
-      } else {
-        pf[it] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  }
+// One chunk's loads, in registers.
+template <typename IT, int K, int V, bool DELTA>
+struct HPrefetch {
+  using C = HCfg<IT, K, V, DELTA>;
+  u32x4 k[C::kKLoads];
+  u32x4 w[DELTA ? C::kKLoads : 1];
+  u32x4 u[C::kULoads];
+  u32x4 g;  // 4 gate values (threads 0..15)
+};
+
+__device__ __forceinline__ const char* cptr(const void* p, int64_t byte_off) {
+  return reinterpret_cast<const char*>(p) + byte_off;
 }
 
-template <typename IT, int K, int BV, bool DELTA>
-__device__ __forceinline__ void h_commit(const u32x4* pf,
-                                         const HStage<IT, K, BV, DELTA>& st) {
-  using C = HCfg<IT, K, BV, DELTA>;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int it = 0; it < C::kPer; ++it) {
-    const int q = tid + it * C::kThreads;
-    if (q >= C::kChunks) break;
-    if (q < C::kKChunks + C::kWChunks) {
-      const bool isw = q >= C::kKChunks;
-      const int qq = isw ? q - C::kKChunks : q;
-      constexpr int CPR = K / C::kVE;
-      const int j = qq / CPR;
-      const int col = (qq - j * CPR) * C::kVE;
-      const int off = j * C::kKPitch + col;
-      if constexpr (C::kSplit) {
-        float vals[4];
-        unpack16(pf[it], vals, 0.f);
-        lds_put4((isw ? st.whi : st.khi) + off, (isw ? st.wlo : st.klo) + off, vals, true);
-      } else {
-        *reinterpret_cast<u32x4*>((isw ? st.whi : st.khi) + off) = pf[it];
-      }
-    } else if (q < C::kKChunks + C::kWChunks + C::kUChunks) {
-      const int qq = q - C::kKChunks - C::kWChunks;
-      constexpr int CPR = BV / C::kVE;
-      const int j = qq / CPR;
-      const int col = (qq - j * CPR) * C::kVE;
-      *reinterpret_cast<u32x4*>(st.u + j * C::kUPitch + col) = pf[it];
-    } else {
-      const int j0 = (q - C::kKChunks - C::kWChunks - C::kUChunks) * 4;
-      *reinterpret_cast<u32x4*>(st.g + j0) = pf[it];
-    }
-  }
-}
-
-template <typename IT, int K, int BV, bool DELTA>
-__global__ void __launch_bounds__(BV / 16 * 64)
+template <typename IT, int K, int V, bool DELTA>
+__global__ void __launch_bounds__(kHThreads)
 chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT* __restrict__ vu,
                    const float* __restrict__ g, const float* __restrict__ h0,
                    float* __restrict__ hout, IT* __restrict__ vnew, float* __restrict__ ht,
-                   int64_t T, int64_t H, int64_t V, int64_t NT, int64_t BH, int n_vt) {
-  using C = HCfg<IT, K, BV, DELTA>;
-  using St = HStage<IT, K, BV, DELTA>;
+                   int64_t T, int64_t H, int64_t NT, int64_t BH) {
+  using C = HCfg<IT, K, V, DELTA>;
+  using St = HStage<IT>;
+  using Pf = HPrefetch<IT, K, V, DELTA>;
+  constexpr int KB = K / 16;
+  constexpr int NVT = V / kHBV;
+  constexpr int EB = C::kEB;
   __shared__ __attribute__((aligned(16))) bf16 lds_b[C::kStages * C::kBf16PerStage];
   __shared__ __attribute__((aligned(16))) IT lds_u[C::kStages * C::kUTile];
   __shared__ __attribute__((aligned(16))) float lds_g[C::kStages * kBT];
@@ -162,16 +107,15 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
   int64_t bh, vt;
   if (BH % 8 == 0) {
     const int64_t xcd = blk % 8, slot = blk / 8;
-    bh = (slot / n_vt) * 8 + xcd;
-    vt = slot % n_vt;
+    bh = (slot / NVT) * 8 + xcd;
+    vt = slot % NVT;
   } else {
-    bh = blk / n_vt;
-    vt = blk % n_vt;
+    bh = blk / NVT;
+    vt = blk % NVT;
   }
   const int64_t b = bh / H, hh = bh % H;
-  const int64_t v0 = vt * BV;
+  const int v0 = (int)vt * kHBV;
 
-  // Stage i's tiles, by pointer arithmetic (no dynamically indexed array).
   auto stage = [&](int i) {
     St st;
     bf16* base = lds_b + i * C::kBf16PerStage;
@@ -189,37 +133,113 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
   const int lane = tid & 63;
   const int grp = lane >> 4;
   const int li = lane & 15;
-  const int ucol = 16 * wv + li;   // column within the V-tile
-  const int64_t vcol = v0 + ucol;  // column within V
-  constexpr int KB = K / 16;
+  const int ucol = 16 * wv + li;  // column within the V-tile
+  const int vcol = v0 + ucol;     // column within V
 
-  // State: S[kappa = 16 kb + 4 grp + r][vcol] in s[kb][r].
-  f32x4 S[KB];
+  // ---- per-lane offsets, fixed for the whole sequence ----------------------
+  // Token t of chunk c, head hh lives at element ((b*T + c*64 + t) * H + hh) * D.
+  const int64_t tok_stride_k = H * K * EB;  // bytes between tokens of k / w
+  const int64_t tok_stride_v = H * V * EB;  // bytes between tokens of u / v / v_new
+  const int kj0 = tid / C::kKCPR, kcol = (tid % C::kKCPR) * C::kVE;
+  const int uj0 = tid / C::kUCPR, ucol0 = (tid % C::kUCPR) * C::kVE;
+  const uint32_t koff0 = (uint32_t)(kj0 * tok_stride_k + kcol * EB);
+  const uint32_t kstep = (uint32_t)((kHThreads / C::kKCPR) * tok_stride_k);
+  const uint32_t uoff0 = (uint32_t)(uj0 * tok_stride_v + (v0 + ucol0) * EB);
+  const uint32_t ustep = (uint32_t)((kHThreads / C::kUCPR) * tok_stride_v);
+  const uint32_t goff = (uint32_t)(4 * tid * H * 4);  // threads 0..15: tokens 4 tid .. 4 tid + 3
+  const uint32_t gstep = (uint32_t)(H * 4);
+  // chunk bases (bytes from the tensor start), advanced per chunk
+  const int64_t kc0 = ((b * T) * H + hh) * K * EB;
+  const int64_t uc0 = ((b * T) * H + hh) * V * EB;
+  const int64_t gc0 = ((b * T) * H + hh) * 4;
+  const int64_t kcs = kBT * tok_stride_k, ucs = kBT * tok_stride_v, gcs = kBT * H * 4;
+
+  auto prefetch = [&](Pf& pf, int64_t c) {
+    const char* kb = cptr(k, kc0 + c * kcs);
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
+    for (int it = 0; it < C::kKLoads; ++it) pf.k[it] = ldg16(kb + koff0 + it * kstep);
+    if constexpr (DELTA) {
+      const char* wb = cptr(w, kc0 + c * kcs);
+#pragma unroll
+      for (int it = 0; it < C::kKLoads; ++it) pf.w[it] = ldg16(wb + koff0 + it * kstep);
+    }
+    const char* ub = cptr(vu, uc0 + c * ucs);
+#pragma unroll
+    for (int it = 0; it < C::kULoads; ++it) pf.u[it] = ldg16(ub + uoff0 + it * ustep);
+    if (tid < kBT / 4) {
+      if (g) {
+        const char* gb = cptr(g, gc0 + c * gcs);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pf.g[e] = *reinterpret_cast<const uint32_t*>(gb + goff + e * gstep);
+      } else {
+        pf.g = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto commit = [&](const Pf& pf, const St& st) {
+#pragma unroll
+    for (int it = 0; it < C::kKLoads; ++it) {
+      const int off = (kj0 + it * (kHThreads / C::kKCPR)) * C::kKPitch + kcol;
+      if constexpr (C::kSplit) {
+        float vals[4];
+        unpack16(pf.k[it], vals, 0.f);
+        lds_put4(st.khi + off, st.klo + off, vals, true);
+        if constexpr (DELTA) {
+          unpack16(pf.w[it], vals, 0.f);
+          lds_put4(st.whi + off, st.wlo + off, vals, true);
+        }
+      } else {
+        *reinterpret_cast<u32x4*>(st.khi + off) = pf.k[it];
+        if constexpr (DELTA) *reinterpret_cast<u32x4*>(st.whi + off) = pf.w[it];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < C::kULoads; ++it) {
+      const int off = (uj0 + it * (kHThreads / C::kUCPR)) * C::kUPitch + ucol0;
+      *reinterpret_cast<u32x4*>(st.u + off) = pf.u[it];
+    }
+    if (tid < kBT / 4) *reinterpret_cast<u32x4*>(st.g + 4 * tid) = pf.g;
+  };
+
+  // State: S[kappa = 16 kb + 4 grp + r][vcol] in S[kb][r].
+  f32x4 S[KB];
+  const uint32_t s_off = (uint32_t)((4 * grp * V + vcol) * 4);  // + (16 kb + r) * V * 4
+  const int64_t st_base = bh * (int64_t)(K * V) * 4;             // h0 / ht (bytes)
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      S[kb][r] = h0 ? h0[(bh * K + 16 * kb + 4 * grp + r) * V + vcol] : 0.f;
-  }
+      S[kb][r] = h0 ? *reinterpret_cast<const float*>(cptr(h0, st_base) + s_off + (16 * kb + r) * V * 4) : 0.f;
 
-  // One chunk of work on the tiles staged in `cs`.
-  auto chunk = [&](const St& cs, int64_t c) {
-    const int64_t tok0 = b * T + c * kBT;
-    float* hc = hout + ((b * NT + c) * H + hh) * (int64_t)K * V;
-    if constexpr (DELTA) {
+  // v_new rows j = 16 jb + 4 grp + r of this lane's column, relative to the chunk base.
+  const uint32_t vn_off = (uint32_t)(4 * grp * tok_stride_v + vcol * EB);
+  auto store_state = [&](int64_t c) {
+    char* hb = reinterpret_cast<char*>(hout) + ((b * NT + c) * H + hh) * (int64_t)(K * V) * 4;
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) hc[(16 * kb + 4 * grp + r) * V + vcol] = S[kb][r];
-    }
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<float*>(hb + s_off + (16 * kb + r) * V * 4) = S[kb][r];
+  };
+
+  Pf pf;
+  if (NT > 0) {
+    prefetch(pf, 0);
+    commit(pf, stage(0));
+    lds_barrier();
+  }
+  for (int64_t c = 0; c < NT; ++c) {
+    const St cs = stage((int)(c % C::kStages));
+    if (c + 1 < NT) prefetch(pf, c + 1);
+    if constexpr (DELTA) store_state(c);  // state before chunk c
 
     // v_new (or v) for rows j = 16 jb + 4 grp + r of this lane's column.
     f32x4 vn[4];
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
+    for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) vn[jb][r] = to_f32(cs.u[(16 * jb + 4 * grp + r) * C::kUPitch + ucol]);
-    }
+
     if constexpr (DELTA) {
       // P1: B operand = S pairs (kappa blocks 2s, 2s+1) in paired order.
       bf16x8 sh[K / 32], sl[K / 32];
@@ -247,11 +267,12 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
         vn[jb] -= a;
       }
       if (vnew) {
+        char* vb = reinterpret_cast<char*>(vnew) + (((b * T + c * kBT) * H + hh) * V) * EB;
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            vnew[((tok0 + 16 * jb + 4 * grp + r) * H + hh) * V + vcol] = from_f32<IT>(vn[jb][r]);
+            *reinterpret_cast<IT*>(vb + vn_off + (16 * jb + r) * tok_stride_v) = from_f32<IT>(vn[jb][r]);
       }
     }
 
@@ -286,75 +307,44 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
         }
       }
     }
-    if constexpr (!DELTA) {
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) hc[(16 * kb + 4 * grp + r) * V + vcol] = S[kb][r];
-    }
+    if constexpr (!DELTA) store_state(c);  // state after chunk c
 
-  };
-
-  // The next chunk's loads are issued before the current chunk computes and
-  // written to the other LDS stage after it.
-  u32x4 pf[C::kPer];
-  if (NT > 0) {
-    h_prefetch<IT, K, BV, DELTA>(pf, k, w, vu, g, b * T, H, hh, V, v0);
-    h_commit<IT, K, BV, DELTA>(pf, stage(0));
-    __syncthreads();
-  }
-  for (int64_t c = 0; c < NT; ++c) {
-    if (c + 1 < NT) h_prefetch<IT, K, BV, DELTA>(pf, k, w, vu, g, b * T + (c + 1) * kBT, H, hh, V, v0);
-    chunk(stage((int)(c % C::kStages)), c);
     if (c + 1 < NT) {
-      if constexpr (C::kStages == 1) __syncthreads();  // every wave is done with the stage
-      h_commit<IT, K, BV, DELTA>(pf, stage((int)((c + 1) % C::kStages)));
+      if constexpr (C::kStages == 1) lds_barrier();  // every wave is done with the stage
+      commit(pf, stage((int)((c + 1) % C::kStages)));
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   if (ht) {
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ht[(bh * K + 16 * kb + 4 * grp + r) * V + vcol] = S[kb][r];
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<float*>(reinterpret_cast<char*>(ht) + st_base + s_off + (16 * kb + r) * V * 4) = S[kb][r];
   }
 }
 
-template <typename IT, int K, int BV, bool DELTA>
+template <typename IT, int K, int V, bool DELTA>
 hipError_t launch_h(const void* k, const void* w, const void* vu, const void* g, const void* h0,
-                    void* h, void* vnew, void* ht, int64_t B, int64_t T, int64_t H, int64_t V,
-                    hipStream_t s) {
-  using C = HCfg<IT, K, BV, DELTA>;
+                    void* h, void* vnew, void* ht, int64_t B, int64_t T, int64_t H, hipStream_t s) {
   const int64_t NT = T / kBT;
-  const int n_vt = (int)(V / BV);
   const int64_t BH = B * H;
-  hipLaunchKernelGGL((chunk_fwd_h_kernel<IT, K, BV, DELTA>), dim3((unsigned)(BH * n_vt)),
-                     dim3(C::kThreads), 0, s, (const IT*)k, (const IT*)w, (const IT*)vu,
-                     (const float*)g, (const float*)h0, (float*)h, (IT*)vnew, (float*)ht, T, H, V,
-                     NT, BH, n_vt);
+  hipLaunchKernelGGL((chunk_fwd_h_kernel<IT, K, V, DELTA>), dim3((unsigned)(BH * (V / kHBV))),
+                     dim3(kHThreads), 0, s, (const IT*)k, (const IT*)w, (const IT*)vu,
+                     (const float*)g, (const float*)h0, (float*)h, (IT*)vnew, (float*)ht, T, H,
+                     NT, BH);
   return hipGetLastError();
 }
 
-// V-tiles of 64 columns (4 wavefronts): the four waves share the staging of
-// each chunk's k / w / u, which keeps the per-thread prefetch buffer small.
-template <typename IT, int K, bool DELTA>
-hipError_t dispatch_bv(int64_t V, const void* k, const void* w, const void* vu, const void* g,
-                       const void* h0, void* h, void* vnew, void* ht, int64_t B, int64_t T,
-                       int64_t H, hipStream_t s) {
-  return launch_h<IT, K, 64, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, V, s);
-}
-
-template <typename IT>
-hipError_t dispatch_h(int64_t K, bool delta, int64_t V, const void* k, const void* w,
-                      const void* vu, const void* g, const void* h0, void* h, void* vnew,
-                      void* ht, int64_t B, int64_t T, int64_t H, hipStream_t s) {
-  if (K == 64) {
-    return delta ? dispatch_bv<IT, 64, true>(V, k, w, vu, g, h0, h, vnew, ht, B, T, H, s)
-                 : dispatch_bv<IT, 64, false>(V, k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
-  }
-  return delta ? dispatch_bv<IT, 128, true>(V, k, w, vu, g, h0, h, vnew, ht, B, T, H, s)
-               : dispatch_bv<IT, 128, false>(V, k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+template <typename IT, bool DELTA>
+hipError_t dispatch_kv(int64_t K, int64_t V, const void* k, const void* w, const void* vu,
+                       const void* g, const void* h0, void* h, void* vnew, void* ht, int64_t B,
+                       int64_t T, int64_t H, hipStream_t s) {
+  if (K == 64 && V == 64) return launch_h<IT, 64, 64, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+  if (K == 64 && V == 128) return launch_h<IT, 64, 128, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+  if (K == 128 && V == 64) return launch_h<IT, 128, 64, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+  return launch_h<IT, 128, 128, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
 }
 
 }  // namespace
@@ -384,9 +374,17 @@ extern "C" int thm_chunk_fwd_h(const void* k, const void* w, const void* vu, con
     if (p && ((uintptr_t)p % 4)) return THM_ERR_MISALIGNED;
   if (v_new && kv_dtype == THM_DTYPE_BF16 && ((uintptr_t)v_new % 2)) return THM_ERR_MISALIGNED;
   if (B > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  // Per-lane offsets within one chunk's token block are 32-bit.
+  if (64 * H * (K > V ? K : V) * (kv_dtype == THM_DTYPE_F32 ? 4 : 2) > (INT64_C(1) << 31))
+    return THM_ERR_UNSUPPORTED;
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = (kv_dtype == THM_DTYPE_F32)
-                     ? dispatch_h<float>(K, delta, V, k, w, vu, g, h0, h, v_new, ht, B, T, H, s)
-                     : dispatch_h<bf16>(K, delta, V, k, w, vu, g, h0, h, v_new, ht, B, T, H, s);
+  hipError_t e;
+  if (kv_dtype == THM_DTYPE_F32) {
+    e = delta ? dispatch_kv<float, true>(K, V, k, w, vu, g, h0, h, v_new, ht, B, T, H, s)
+              : dispatch_kv<float, false>(K, V, k, w, vu, g, h0, h, v_new, ht, B, T, H, s);
+  } else {
+    e = delta ? dispatch_kv<bf16, true>(K, V, k, w, vu, g, h0, h, v_new, ht, B, T, H, s)
+              : dispatch_kv<bf16, false>(K, V, k, w, vu, g, h0, h, v_new, ht, B, T, H, s);
+  }
   return (int)e;
 }

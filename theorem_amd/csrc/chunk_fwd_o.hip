@@ -154,7 +154,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     lds_put4(hhi + r * C::kPitch + col, hlo + r * C::kPitch + col, vals, C::kSplit);
   }
   if (tid < kBT) gs[tid] = gload;
-  __syncthreads();
+  lds_barrier();
 
   bf16x8 qh[KS], ql[KS];
 #pragma unroll

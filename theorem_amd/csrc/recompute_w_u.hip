@@ -109,7 +109,7 @@ recompute_w_u_kernel(const IT* __restrict__ k, const IT* __restrict__ v,
     sbeta[tid] = bj;
     sg[tid] = gj;
   }
-  __syncthreads();
+  lds_barrier();
 
   // 3. Scaled A operands: A'[t][j] for j = 32 s + 8 grp + 0..7.
   bf16x8 awh[2], awl[2], auh[2], aul[2];
