@@ -127,6 +127,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--small", action="store_true", help="1/8-size workload (quick check)")
+    ap.add_argument("--only", choices=["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o"],
+                    help="run only this kernel of the step (for per-kernel rocprofv3 counter runs)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="run a plain 1 GiB device-to-device copy (rocprofv3 counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the hot-path kernels are single-device; "
@@ -135,6 +139,17 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.copy_calib:
+        # A plain copy kernel of known size: FETCH_SIZE / WRITE_SIZE per dispatch
+        # should read 1 GiB each; the ratio calibrates the counters.
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes": src.numel() * 4, "launches": args.warmup + args.steps}))
+        return 0
 
     from theorem_amd import configs
     from theorem_amd.kernels import causal_conv1d, chunk_fwd_h, chunk_fwd_o, recompute_w_u
@@ -168,6 +183,25 @@ def main() -> int:
         o = chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=vn, g=g, h=h, scale=scale))
         mark(4)
         return y, o, ht
+
+    if args.only:
+        # One kernel, W + K launches on inputs from one full step (counter runs).
+        y, o, ht = step()
+        w, u = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V))
+        h, vn, _ = chunk_fwd_h.custom_kernel(dict(k=k, w=w, u=u, g=g, output_final_state=True))
+        torch.cuda.synchronize()
+        run = {
+            "causal_conv1d": lambda: causal_conv1d.custom_kernel(conv_in),
+            "recompute_w_u": lambda: recompute_w_u.custom_kernel(
+                recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V)),
+            "chunk_fwd_h": lambda: chunk_fwd_h.custom_kernel(dict(k=k, w=w, u=u, g=g, output_final_state=True)),
+            "chunk_fwd_o": lambda: chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=vn, g=g, h=h, scale=scale)),
+        }[args.only]
+        for _ in range(args.warmup + args.steps):
+            run()
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "launches": args.warmup + args.steps + 1}))
+        return 0
 
     for _ in range(args.warmup):
         step()

@@ -78,14 +78,14 @@ struct HPrefetch {
   u32x4 k[C::kKLoads];
   u32x4 w[DELTA ? C::kKLoads : 1];
   u32x4 u[C::kULoads];
-  u32x4 g;  // 4 gate values (threads 0..15)
+  float g;  // gate of token lane_id() of the chunk
 };
 
 __device__ __forceinline__ const char* cptr(const void* p, int64_t byte_off) {
   return reinterpret_cast<const char*>(p) + byte_off;
 }
 
-template <typename IT, int K, int V, bool DELTA>
+template <typename IT, int K, int V, bool DELTA, bool HAS_G>
 __global__ void __launch_bounds__(kHThreads)
 chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT* __restrict__ vu,
                    const float* __restrict__ g, const float* __restrict__ h0,
@@ -146,8 +146,7 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
   const uint32_t kstep = (uint32_t)((kHThreads / C::kKCPR) * tok_stride_k);
   const uint32_t uoff0 = (uint32_t)(uj0 * tok_stride_v + (v0 + ucol0) * EB);
   const uint32_t ustep = (uint32_t)((kHThreads / C::kUCPR) * tok_stride_v);
-  const uint32_t goff = (uint32_t)(4 * tid * H * 4);  // threads 0..15: tokens 4 tid .. 4 tid + 3
-  const uint32_t gstep = (uint32_t)(H * 4);
+  const uint32_t goff = (uint32_t)(lane * H * 4);  // every wave: token `lane` of the chunk
   // chunk bases (bytes from the tensor start), advanced per chunk
   const int64_t kc0 = ((b * T) * H + hh) * K * EB;
   const int64_t uc0 = ((b * T) * H + hh) * V * EB;
@@ -166,15 +165,11 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
     const char* ub = cptr(vu, uc0 + c * ucs);
 #pragma unroll
     for (int it = 0; it < C::kULoads; ++it) pf.u[it] = ldg16(ub + uoff0 + it * ustep);
-    if (tid < kBT / 4) {
-      if (g) {
-        const char* gb = cptr(g, gc0 + c * gcs);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pf.g[e] = *reinterpret_cast<const uint32_t*>(gb + goff + e * gstep);
-      } else {
-        pf.g = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
+    // Every wave loads the chunk's 64 gates (one per lane): no branch around a
+    // memory operation, so the chunk loop issues the same VMEM sequence on
+    // every path and the waits at the commit cover exactly the prefetch.
+    if constexpr (HAS_G) pf.g = *reinterpret_cast<const float*>(cptr(g, gc0 + c * gcs) + goff);
+    else pf.g = 0.f;
   };
   auto commit = [&](const Pf& pf, const St& st) {
 #pragma unroll
@@ -198,7 +193,7 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
       const int off = (uj0 + it * (kHThreads / C::kUCPR)) * C::kUPitch + ucol0;
       *reinterpret_cast<u32x4*>(st.u + off) = pf.u[it];
     }
-    if (tid < kBT / 4) *reinterpret_cast<u32x4*>(st.g + 4 * tid) = pf.g;
+    if (wv == 0) st.g[lane] = pf.g;
   };
 
   // State: S[kappa = 16 kb + 4 grp + r][vcol] in S[kb][r].
@@ -266,14 +261,6 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
         }
         vn[jb] -= a;
       }
-      if (vnew) {
-        char* vb = reinterpret_cast<char*>(vnew) + (((b * T + c * kBT) * H + hh) * V) * EB;
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            *reinterpret_cast<IT*>(vb + vn_off + (16 * jb + r) * tok_stride_v) = from_f32<IT>(vn[jb][r]);
-      }
     }
 
     // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
@@ -314,6 +301,18 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
       commit(pf, stage((int)((c + 1) % C::kStages)));
     }
     lds_barrier();
+    // v_new after the commit: stores queued behind the prefetch would make its
+    // wait cover them too (loads and stores share one in-order counter).
+    if constexpr (DELTA) {
+      if (vnew) {
+        char* vb = reinterpret_cast<char*>(vnew) + (((b * T + c * kBT) * H + hh) * V) * EB;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<IT*>(vb + vn_off + (16 * jb + r) * tok_stride_v) = from_f32<IT>(vn[jb][r]);
+      }
+    }
   }
 
   if (ht) {
@@ -330,10 +329,16 @@ hipError_t launch_h(const void* k, const void* w, const void* vu, const void* g,
                     void* h, void* vnew, void* ht, int64_t B, int64_t T, int64_t H, hipStream_t s) {
   const int64_t NT = T / kBT;
   const int64_t BH = B * H;
-  hipLaunchKernelGGL((chunk_fwd_h_kernel<IT, K, V, DELTA>), dim3((unsigned)(BH * (V / kHBV))),
-                     dim3(kHThreads), 0, s, (const IT*)k, (const IT*)w, (const IT*)vu,
-                     (const float*)g, (const float*)h0, (float*)h, (IT*)vnew, (float*)ht, T, H,
-                     NT, BH);
+  const dim3 grid((unsigned)(BH * (V / kHBV)));
+  if (g) {
+    hipLaunchKernelGGL((chunk_fwd_h_kernel<IT, K, V, DELTA, true>), grid, dim3(kHThreads), 0, s,
+                       (const IT*)k, (const IT*)w, (const IT*)vu, (const float*)g, (const float*)h0,
+                       (float*)h, (IT*)vnew, (float*)ht, T, H, NT, BH);
+  } else {
+    hipLaunchKernelGGL((chunk_fwd_h_kernel<IT, K, V, DELTA, false>), grid, dim3(kHThreads), 0, s,
+                       (const IT*)k, (const IT*)w, (const IT*)vu, (const float*)g, (const float*)h0,
+                       (float*)h, (IT*)vnew, (float*)ht, T, H, NT, BH);
+  }
   return hipGetLastError();
 }
 

@@ -55,8 +55,8 @@ struct RowFrag {
 template <typename IT>
 __device__ __forceinline__ RowFrag<IT> load_frag(const IT* p) {
   RowFrag<IT> f;
-  f.r[0] = ldg16(p);
-  if constexpr (sizeof(IT) == 4) f.r[1] = ldg16(p + 4);
+  f.r[0] = ldg16_nt(p);
+  if constexpr (sizeof(IT) == 4) f.r[1] = ldg16_nt(p + 4);
   return f;
 }
 
@@ -107,7 +107,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     const int qi = tid + it * kOThreads;
     const int j = qi / C::kVCPR;
     const int col = (qi - j * C::kVCPR) * C::kVE;
-    vr[it] = ldg16(v + ((tok0 + j) * H + hh) * V + col);
+    vr[it] = ldg16_nt(v + ((tok0 + j) * H + hh) * V + col);
   }
   const float* hsrc = hs + ((b * NT + c) * H + hh) * (int64_t)(K * V);
 #pragma unroll
@@ -115,7 +115,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     const int qi = tid + it * kOThreads;
     const int r = qi / (V / 4);
     const int col = (qi - r * (V / 4)) * 4;
-    hr[it] = ldg16(hsrc + r * V + col);
+    hr[it] = ldg16_nt(hsrc + r * V + col);
   }
   // q fragments q[i][32 s + 8 grp + 0..7] and k fragments of key blocks jb <= wv.
   RowFrag<IT> qf[KS], kf[4][KS];

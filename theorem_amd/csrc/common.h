@@ -90,6 +90,12 @@ __device__ __forceinline__ void stg16_nt(void* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+// Non-temporal (streaming) scalar loads / stores: data read or written once.
+template <typename T>
+__device__ __forceinline__ T ldg_nt(const T* p) { return __builtin_nontemporal_load(p); }
+template <typename T>
+__device__ __forceinline__ void stg_nt(T* p, T v) { __builtin_nontemporal_store(v, p); }
+
 // Unpack 16 bytes into floats: 4 fp32 or 8 bf16.
 __device__ __forceinline__ void unpack16(u32x4 r, float* out, float /*tag*/) {
   out[0] = __uint_as_float(r[0]);

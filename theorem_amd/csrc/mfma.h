@@ -94,13 +94,13 @@ __device__ __forceinline__ void split_bf16x8(const float* v, bf16x8& hi, bf16x8&
 }
 
 // Load 8 consecutive elements of type T (16-byte aligned for bf16, 32-byte for
-// fp32) as floats.
-__device__ __forceinline__ void load8f(const bf16* p, float* v) {
-  unpack16(ldg16(p), v, bf16{});
+// fp32) as floats; `nt` selects a non-temporal (streaming) load.
+__device__ __forceinline__ void load8f(const bf16* p, float* v, bool nt = false) {
+  unpack16(nt ? ldg16_nt(p) : ldg16(p), v, bf16{});
 }
-__device__ __forceinline__ void load8f(const float* p, float* v) {
-  unpack16(ldg16(p), v, 0.f);
-  unpack16(ldg16(p + 4), v + 4, 0.f);
+__device__ __forceinline__ void load8f(const float* p, float* v, bool nt = false) {
+  unpack16(nt ? ldg16_nt(p) : ldg16(p), v, 0.f);
+  unpack16(nt ? ldg16_nt(p + 4) : ldg16(p + 4), v + 4, 0.f);
 }
 // Paired order: elements [k0 + 4g, +4) and [k0 + 16 + 4g, +4).
 __device__ __forceinline__ void load8f_paired(const bf16* row, int k0, float* v) {
@@ -122,7 +122,9 @@ __device__ __forceinline__ void load8f_paired(const float* row, int k0, float* v
   v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
 }
 
-// Store 4 consecutive outputs (16 bytes fp32 / 8 bytes bf16).
+// Store 4 consecutive outputs (16 bytes fp32 / 8 bytes bf16).  Plain stores:
+// these partial-line writes rely on L2 write-combining, which streaming
+// (non-temporal) stores bypass.
 __device__ __forceinline__ void store4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 __device__ __forceinline__ void store4(bf16* p, f32x4 v) {
   bf16x4 r;

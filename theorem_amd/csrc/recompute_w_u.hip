@@ -83,7 +83,7 @@ recompute_w_u_kernel(const IT* __restrict__ k, const IT* __restrict__ v,
   const float* arow = A + trow * kBT;
   float av[2][8];
 #pragma unroll
-  for (int s = 0; s < 2; ++s) load8f(arow + 32 * s + 8 * grp, av[s]);
+  for (int s = 0; s < 2; ++s) load8f(arow + 32 * s + 8 * grp, av[s], false);
   float bj = 0.f, gj = 0.f;
   if (tid < kBT) {
     const int64_t row = (tok0 + tid) * H + h;
