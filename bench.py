@@ -2,7 +2,7 @@
 DeltaNet chunk forward (recompute_w_u -> chunk_fwd_h -> chunk_fwd_o) at
 BASELINE.json config 4 (the largest single-GPU configuration), bf16.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--small]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-shapes] [--small]
 
 Prints ONE JSON line (rank 0).  ``value`` is microseconds per step (all four
 kernels, inputs resident in HBM, outputs preallocated by the caching
@@ -13,7 +13,8 @@ algorithmic bytes per launch / its average duration vs 8 TB/s.  ``traffic``
 is read from profiles/traffic_cfg4.json when that summary of rocprofv3
 FETCH_SIZE / WRITE_SIZE runs exists, else null.  ``cpu_baseline`` times the
 CPU oracle on a bounded sample (one batch element of the same workload) and
-scales to a full step.
+scales to a full step.  ``shapes`` gives each kernel's latency at configs 0-3,
+the shapes the reference publishes numbers for.
 """
 from __future__ import annotations
 
@@ -118,6 +119,77 @@ def cpu_baseline(torch, inputs, conv_inputs, target_s: float = 12.0):
                        f"chain {1e3 * chain_s:.0f} ms")}
 
 
+# --------------------------------------------------------------------------- per-shape latency
+
+def shape_latencies(torch, dev, warmup: int = 5, iters: int = 50, batched: int = 200):
+    """Latency of each kernel at BASELINE.json configs 0-3 (the reference's
+    published shapes), three ways:
+      us_ref       the reference's protocol (benchmarks/pytorch_baseline.py:72-96):
+                   min over ``iters`` calls, each an event pair around
+                   ``custom_kernel`` on an idle GPU, so the host-side launch
+                   (Python wrapper + ctypes + HIP launch) is inside the bracket;
+      us_cold_*    min / p50 with a 512 MiB write before each call: the start
+                   event runs after that write, by which time the launch is
+                   queued, so this is the kernel on cold caches;
+      us_batched   ``batched`` back-to-back calls under one event pair, per call
+                   (bounded below by the host launch rate for tiny kernels)."""
+    from theorem_amd import configs
+    from theorem_amd.kernels import causal_conv1d, chunk_fwd_h, chunk_fwd_o, recompute_w_u
+
+    flush = torch.empty(1 << 27, dtype=torch.float32, device=dev)
+    c0 = configs.make_conv_inputs(1, 2560, 4096, 4, dtype=torch.float32, seed=0, device=dev)
+    w1 = configs.make_wu_inputs(2, 512, 3, 64, 64, seed=0, device=dev)
+    o2 = configs.make_o_inputs(2, 512, 3, 64, 64, seed=0, device=dev)
+    h3 = configs.make_h_inputs(2, 1024, 3, 64, 64, seed=0, device=dev)
+    wu_data = recompute_w_u.Data(**w1, B=2, T=512, H=3, K=64, V=64)
+    cases = [
+        ("cfg0", "causal_conv1d", "(1,2560,4096,W=4) fp32", lambda: causal_conv1d.custom_kernel(c0),
+         work_conv(1, 2560, 4096, 4, eb=4, ebw=4)),
+        ("cfg1", "recompute_w_u", "(2,512,3,64,64) bf16", lambda: recompute_w_u.custom_kernel(wu_data),
+         work_wu(2, 512, 3, 64, 64)),
+        ("cfg2", "chunk_fwd_o", "(2,512,3,64,64) bf16",
+         lambda: chunk_fwd_o.custom_kernel(dict(q=o2["q"], k=o2["k"], v=o2["v"], g=o2["g"], h=o2["h"],
+                                                scale=o2["scale"])),
+         work_o(2, 512, 3, 64, 64)),
+        ("cfg3", "chunk_fwd_h", "(2,1024,3,64,64) bf16 delta form, h0 = 0",
+         lambda: chunk_fwd_h.custom_kernel(dict(k=h3["k"], w=h3["w"], u=h3["u"], g=h3["g"],
+                                                output_final_state=True)),
+         work_h(2, 1024, 3, 64, 64)),
+    ]
+    out = {}
+    for cfg, name, shape, fn, (by, fl) in cases:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        def timed(pre):
+            ts = []
+            for _ in range(iters):
+                if pre is not None:
+                    pre()
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                fn()
+                e.record()
+                torch.cuda.synchronize()
+                ts.append(s.elapsed_time(e) * 1e3)
+            return sorted(ts)
+        ref = timed(None)
+        cold = timed(flush.zero_)
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(batched):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        bat = s.elapsed_time(e) * 1e3 / batched
+        out[cfg] = {"kernel": name, "shape": shape, "us_ref": round(ref[0], 2),
+                    "us_cold_min": round(cold[0], 2), "us_cold_p50": round(cold[len(cold) // 2], 2),
+                    "us_batched": round(bat, 2), "bytes": by, "flops": fl,
+                    "hbm_frac_cold_min": round(by / (cold[0] * 1e-6) / HBM_PEAK, 4)}
+    del flush
+    return out
+
+
 # --------------------------------------------------------------------------- main
 
 def main() -> int:
@@ -126,6 +198,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape latencies of configs 0-3")
     ap.add_argument("--small", action="store_true", help="1/8-size workload (quick check)")
     ap.add_argument("--only", choices=["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o"],
                     help="run only this kernel of the step (for per-kernel rocprofv3 counter runs)")
@@ -134,7 +207,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the hot-path kernels are single-device; "
-              "multi-GPU sharding is described in DESIGN.md but not launched). Use --gpus 1.",
+              "multi-GPU sharding is designed but not launched). Use --gpus 1.",
               file=sys.stderr)
         return 2
 
@@ -243,6 +316,11 @@ def main() -> int:
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
                 "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic}
 
+    shapes = None
+    if not args.no_shapes:
+        print("[bench] per-shape latencies (configs 0-3)", file=sys.stderr, flush=True)
+        shapes = shape_latencies(torch, dev)
+
     cpu = None
     if not args.no_cpu:
         print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
@@ -256,7 +334,7 @@ def main() -> int:
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded torch CPU generator; BASELINE.json config-4 distributions)",
         "config": {"workload": workload, "parallelism": "single GPU"},
-        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu,
+        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu, "shapes": shapes,
     }
     print(json.dumps(line))
     return 0

@@ -82,3 +82,15 @@ def test_mutation_is_caught():
     good = conv.causal_conv1d_c(x, w, None)
     bad = conv.causal_conv1d_c(x, w[:, ::-1].copy(), None)
     assert good[0, 0, 4] == 3.0 and not np.array_equal(good, bad)
+
+
+def test_silu_pins():
+    # silu(x) = x * sigmoid(x): torch's library routine, the fixed point
+    # silu(0) = 0, the limits x (x -> +inf) and 0 (x -> -inf), and
+    # silu(x) - silu(-x) = x (an odd-part identity a sign slip breaks).
+    x = np.linspace(-30, 30, 2001)
+    got = conv.silu(x)
+    np.testing.assert_allclose(got, F.silu(torch.from_numpy(x)).numpy(), rtol=1e-12, atol=1e-12)
+    assert conv.silu(np.array([0.0]))[0] == 0.0
+    np.testing.assert_allclose(conv.silu(np.array([40.0, -40.0])), [40.0, 0.0], atol=1e-12)
+    np.testing.assert_allclose(got - conv.silu(-x), x, atol=1e-12)
