@@ -9,8 +9,11 @@
 //                              LDS array holding lds[i] = i) -> out[64][4] int16
 //   probe_dpp_wave_shr1      : src[64] int32, old[64] int32 -> out[64] int32
 //   probe_cvt_bf16           : x[n] f32 -> y[n] bf16 (n even, n <= 4096)
+//   probe_quad_transpose     : x[64][4] f32 -> y[64][4] f32 (thm::quad_transpose)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include "../../theorem_amd/csrc/vmem.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -63,7 +66,15 @@ __global__ void k_cvt(const float* x, bf16x2* y, int npairs) {
   }
 }
 
+__global__ void __launch_bounds__(64) k_quad_transpose(const f32x4* x, f32x4* y) {
+  y[threadIdx.x] = thm::quad_transpose(x[threadIdx.x]);
+}
+
 extern "C" {
+int probe_quad_transpose(const void* x, void* y, void* stream) {
+  hipLaunchKernelGGL(k_quad_transpose, dim3(1), dim3(64), 0, (hipStream_t)stream, (const f32x4*)x, (f32x4*)y);
+  return (int)hipGetLastError();
+}
 int probe_mfma_16x16x32_bf16(const void* a, const void* b, void* c, void* stream) {
   hipLaunchKernelGGL(k_mfma16, dim3(1), dim3(64), 0, (hipStream_t)stream,
                      (const bf16x8*)a, (const bf16x8*)b, (f32x4*)c);

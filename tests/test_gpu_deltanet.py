@@ -179,10 +179,105 @@ def test_h_reference_form_extras(dev):
     assert_close(ht_ref, h_ref[:, -1], 0, 0, "final = last post-update state")
 
 
-def test_h_empty_sequence_final_state(dev):
-    k = torch.empty(1, 0, 2, 64, device=dev)
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("gate", ["logsigmoid", None])
+def test_h_reference_form_bf16(dev, K, V, gate):
+    # bf16 reference form (v used as is, h stored after each chunk), with an
+    # initial and a final state; NT = 5 exercises a ring of stages that does
+    # not divide the chunk count.
+    d = configs.make_h_inputs(2, 320, 3, K, V, seed=8, device=dev, dtype=torch.bfloat16,
+                              gate=gate or "zero", h0_std=0.1)
+    g = d["g"] if gate else None
+    h, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], v=d["u"], g=g, initial_state=d["h0"],
+                                           output_final_state=True))
+    sync()
+    gk = np_(g) if g is not None else None
+    # With an initial state the reference form is the delta form with w = 0,
+    # stored one chunk later (after instead of before each chunk's update).
+    eh_pre, _, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np.zeros_like(np_(d["w"])), np_(d["u"]), gk,
+                                           h0=np_(d["h0"]))
+    eh_post = np.concatenate([eh_pre[:, 1:], eht[:, None]], axis=1)
+    assert_close(h, eh_post, 1e-2, 1e-2, f"h K={K} V={V} gate={gate}")
+    assert_close(ht, eht, 1e-2, 1e-2, f"final K={K} V={V} gate={gate}")
+    # Without one it is the oracle's reference form directly.
+    h_z = chunk_fwd_h.custom_kernel(dict(k=d["k"], v=d["u"], g=g))
+    sync()
+    g0 = gk if gk is not None else np.zeros(d["k"].shape[:3])
+    assert_close(h_z, odn.chunk_fwd_h_ref(np_(d["k"]), np_(d["u"]), g0), 1e-2, 1e-2, f"h0=0 K={K} V={V}")
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (128, 128)])
+def test_h_delta_bf16_without_v_new_and_gate(dev, K, V):
+    # save_new_value=False (no v_new output) and no gate; single chunk and odd chunk counts.
+    for T in (64, 192):
+        d = configs.make_h_inputs(1, T, 2, K, V, seed=9, device=dev, dtype=torch.bfloat16, h0_std=0.1)
+        h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=None, initial_state=d["h0"],
+                                                   output_final_state=True, save_new_value=False))
+        sync()
+        assert vn is None
+        eh, _, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np_(d["w"]), np_(d["u"]), None, h0=np_(d["h0"]))
+        assert_close(h, eh, 1e-2, 1e-2, f"h K={K} V={V} T={T}")
+        assert_close(ht, eht, 1e-2, 1e-2, f"final K={K} V={V} T={T}")
+
+
+# bf16 grids of at least 256 workgroups (B * H * V / 64) run the DMA pipeline
+# kernel; smaller ones the register-prefetch kernel.  These shapes force the
+# former at every K, V and flag combination.
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("form", ["delta", "delta_plain", "reference", "reference_plain"])
+def test_h_dma_pipeline_forms(dev, K, V, form):
+    B, H = 4, (64 if V == 64 else 32)
+    assert B * H * (V // 64) >= 256
+    for T in (192, 64):
+        d = configs.make_h_inputs(B, T, H, K, V, seed=10, device=dev, dtype=torch.bfloat16, h0_std=0.1)
+        plain = form.endswith("plain")
+        g = None if plain else d["g"]
+        h0 = None if plain else d["h0"]
+        gk = np_(g) if g is not None else None
+        h0k = np_(h0) if h0 is not None else None
+        if form.startswith("delta"):
+            h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=g, initial_state=h0,
+                                                       output_final_state=True, save_new_value=not plain))
+            sync()
+            eh, evn, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np_(d["w"]), np_(d["u"]), gk, h0=h0k)
+            if not plain:
+                assert_close(vn, evn, 1e-2, 1e-2, f"v_new {form} K={K} V={V} T={T}")
+            else:
+                assert vn is None
+        else:
+            h, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], v=d["u"], g=g, initial_state=h0,
+                                                   output_final_state=True))
+            sync()
+            pre, _, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np.zeros_like(np_(d["w"])), np_(d["u"]), gk, h0=h0k)
+            eh = np.concatenate([pre[:, 1:], eht[:, None]], axis=1)
+        assert_close(h, eh, 1e-2, 1e-2, f"h {form} K={K} V={V} T={T}")
+        assert_close(ht, eht, 1e-2, 1e-2, f"final {form} K={K} V={V} T={T}")
+
+
+def test_h_dma_pipeline_unaligned_head_count_and_empty(dev):
+    # B * H not a multiple of 8 (the plain block mapping) and T = 0 on the DMA path.
+    B, T, H, K, V = 1, 128, 260, 64, 64
+    d = configs.make_h_inputs(B, T, H, K, V, seed=12, device=dev, dtype=torch.bfloat16, h0_std=0.1)
+    h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=d["g"], initial_state=d["h0"],
+                                               output_final_state=True))
+    sync()
+    eh, evn, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np_(d["w"]), np_(d["u"]), np_(d["g"]), h0=np_(d["h0"]))
+    assert_close(h, eh, 1e-2, 1e-2, "h")
+    assert_close(vn, evn, 1e-2, 1e-2, "v_new")
+    assert_close(ht, eht, 1e-2, 1e-2, "final")
+    k0 = torch.empty(B, 0, H, K, device=dev, dtype=torch.bfloat16)
+    h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=k0, w=k0, u=torch.empty(B, 0, H, V, device=dev, dtype=torch.bfloat16),
+                                               g=None, initial_state=d["h0"], output_final_state=True))
+    sync()
+    assert h.shape == (B, 0, H, K, V)
+    assert_close(ht, d["h0"], 0, 0, "T=0 final state")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_h_empty_sequence_final_state(dev, dtype):
+    k = torch.empty(1, 0, 2, 64, device=dev, dtype=dtype)
     h0 = torch.randn(1, 2, 64, 64, device=dev)
-    h, ht = chunk_fwd_h.custom_kernel(dict(k=k, v=torch.empty(1, 0, 2, 64, device=dev), g=None,
+    h, ht = chunk_fwd_h.custom_kernel(dict(k=k, v=torch.empty(1, 0, 2, 64, device=dev, dtype=dtype), g=None,
                                            initial_state=h0, output_final_state=True))
     sync()
     assert h.shape == (1, 0, 2, 64, 64)

@@ -1,6 +1,7 @@
 """Lane-layout checks of the single gfx950 instructions the kernels are built on
 (tests/csrc/probe.hip): MFMA operand/accumulator layouts, the LDS transpose
-read, the DPP whole-wave shift and the fp32 -> bf16 conversion."""
+read, the DPP whole-wave shift, the fp32 -> bf16 conversion and the quad
+transpose used before the 16-byte state stores."""
 from __future__ import annotations
 
 import ctypes
@@ -103,3 +104,18 @@ def test_bf16_conversion_is_rne(probe, dev):
     yy = y.cpu()
     same = (yy.view(torch.int16) == ref.view(torch.int16)) | (torch.isnan(yy) & torch.isnan(ref))
     assert bool(same.all())
+
+
+def test_quad_transpose(probe, dev):
+    # Lane 4m + q holds row q of a 4x4 block in x[lane][0..3]; afterwards it
+    # must hold column q: y[4m + q][i] = x[4m + i][q].
+    x = (torch.arange(256, dtype=torch.float32).reshape(64, 4) * 1.5 - 7).to(dev)
+    y = torch.empty_like(x)
+    assert probe.probe_quad_transpose(P(x), P(y), S()) == 0
+    torch.cuda.synchronize()
+    xc, yc = x.cpu().numpy(), y.cpu().numpy()
+    exp = np.empty_like(xc)
+    for lane in range(64):
+        for i in range(4):
+            exp[lane, i] = xc[(lane & ~3) + i, lane & 3]
+    np.testing.assert_array_equal(yc, exp)

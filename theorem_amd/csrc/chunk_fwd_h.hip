@@ -25,9 +25,15 @@
 // fixed before the loop, so the loop spends no VALU on address arithmetic.
 // Workgroups map XCD-aware: the V-tiles of one (b, head) share an XCD (and its
 // L2), so k and w are fetched from HBM once per (b, head).
+//
+// bf16 inputs on grids that fill the GPU use a second kernel (below): chunk
+// tiles arrive by global -> LDS DMA instead of through registers, and the K
+// rows of the state are split over two waves per SIMD.
 #include <type_traits>
 
+#include "h_layout.h"
 #include "mfma.h"
+#include "vmem.h"
 
 namespace thm {
 namespace {
@@ -324,6 +330,322 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 inputs: DMA pipeline.
+//
+// One workgroup per (b, head, V-tile of 64 columns) of 4 KS wavefronts: wave
+// w = 4 kh + wq owns state rows [kh K/KS, (kh + 1) K/KS) and columns
+// 16 wq .. 16 wq + 15 of the tile.  Chunk tiles (k, w, u or v, g) are copied
+// global -> LDS by DMA into a ring of NS stages, NS - 1 chunks ahead of use,
+// with no registers held for them; the tiles are stored unpadded with the XOR
+// swizzle of h_layout.h.  Per chunk c:
+//   wait for this wave's DMA of chunk c, barrier A, issue the DMA of chunk
+//   c + NS - 1 into the stage chunk c - 1 used;
+//   delta form: h[c] = S;  P1 v_new = u - w S (with KS = 2 each K half forms a
+//   partial sum, exchanged through LDS behind barrier B);  v_new stored;
+//   P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}) on this wave's rows;
+//   reference form: h[c] = S after P2.
+// h and v_new are written as 16- / 8-byte lane stores after a 4x4 quad
+// transpose of the accumulators.  Every DMA and store of the chunk loop is
+// issued through vmem.h, so the wait at the top of the loop is an exact count:
+// after this wave's DMA of chunk c it has issued NS - 1 chunks of stores and
+// NS - 2 chunks of DMA.
+template <int K, int KS, int NS, bool DELTA, bool HAS_G, bool STORE_VN>
+struct PCfg {
+  static constexpr int kWaves = 4 * KS;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kRowK = K * 2;                   // bytes per k / w row
+  static constexpr int kTileK = kBT * kRowK;            // bytes per k / w tile
+  static constexpr int kRowU = kHBV * 2;                // bytes per u row of the V-tile
+  static constexpr int kTileU = kBT * kRowU;
+  static constexpr int kGBytes = kWaves * kBT * 4;      // one gate copy per wave
+  static constexpr int kStage = kTileK * (DELTA ? 2 : 1) + kTileU + (HAS_G ? kGBytes : 0);
+  static constexpr int kXBytes = (DELTA && KS == 2) ? kWaves * 4 * 64 * 16 : 0;  // P1 partials
+  static constexpr int kLds = NS * kStage + kXBytes;
+  static constexpr int kRows = K / KS;                  // state rows per wave
+  static constexpr int KBH = kRows / 16;                // 16-row accumulator tiles per wave
+  static constexpr int kKDma = kTileK / 1024 / kWaves;  // 1 KiB DMA instructions per wave per k tile
+  static constexpr int kUDma = kTileU / 1024 / kWaves;
+  static constexpr int kJbStore = 4 / KS;               // v_new row tiles stored per wave
+  static constexpr int kDma = kKDma * (DELTA ? 2 : 1) + kUDma + (HAS_G ? 1 : 0);
+  static constexpr int kStores = KBH + ((DELTA && STORE_VN) ? kJbStore : 0);
+  static constexpr int kWaitFirst = (NS - 2) * kDma;
+  static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma;
+  static_assert(KS == 1 || KS == 2, "K split");
+  static_assert(NS >= 2, "at least double buffering");
+  static_assert(kKDma >= 1 && kUDma >= 1, "whole DMA instructions per wave");
+  static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
+  static_assert(kLds <= 160 * 1024, "LDS budget");
+  static_assert(kWaitSteady <= 63, "vmcnt range");
+};
+
+template <int K, int V, int KS, int NS, bool DELTA, bool HAS_G, bool STORE_VN>
+__global__ void __launch_bounds__(256 * KS)
+chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
+                       const bf16* __restrict__ vu, const float* __restrict__ g,
+                       const float* __restrict__ h0, float* __restrict__ hout,
+                       bf16* __restrict__ vnew, float* __restrict__ ht, int64_t T, int64_t H,
+                       int64_t NT, int64_t BH) {
+  using C = PCfg<K, KS, NS, DELTA, HAS_G, STORE_VN>;
+  constexpr int NVT = V / kHBV;
+  __shared__ __attribute__((aligned(1024))) char lds[C::kLds];
+
+  const int64_t blk = blockIdx.x;
+  int64_t bh, vt;
+  if (BH % 8 == 0) {  // the V-tiles of one (b, head) on one XCD (block i runs on XCD i % 8)
+    const int64_t xcd = blk % 8, slot = blk / 8;
+    bh = (slot / NVT) * 8 + xcd;
+    vt = slot % NVT;
+  } else {
+    bh = blk / NVT;
+    vt = blk % NVT;
+  }
+  const int64_t b = bh / H, hh = bh % H;
+  const int v0 = (int)vt * kHBV;
+
+  const int tid = threadIdx.x;
+  const int wi = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = wi >> 2, wq = wi & 3;
+  const int lane = tid & 63, grp = lane >> 4, li = lane & 15;
+  const int kap0 = kh * C::kRows;
+
+  auto stage_k = [&](int s) { return lds + s * C::kStage; };
+  auto stage_w = [&](int s) { return lds + s * C::kStage + C::kTileK; };
+  auto stage_u = [&](int s) { return lds + s * C::kStage + C::kTileK * (DELTA ? 2 : 1); };
+  auto stage_g = [&](int s) {
+    return reinterpret_cast<float*>(lds + s * C::kStage + C::kTileK * (DELTA ? 2 : 1) + C::kTileU);
+  };
+  float* const xbuf = reinterpret_cast<float*>(lds + NS * C::kStage);
+
+  // Global geometry in bytes.  Token t of chunk c, head hh: ((b T + 64 c + t) H + hh) D.
+  const int64_t tsk = H * K * 2, tsv = H * V * 2;
+  const int64_t kc0 = ((b * T) * H + hh) * K * 2;
+  const int64_t uc0 = ((b * T) * H + hh) * V * 2 + v0 * 2;
+  const int64_t gc0 = ((b * T) * H + hh) * 4;
+  const int64_t kcs = kBT * tsk, ucs = kBT * tsv, gcs = kBT * H * 4;
+
+  // Per-lane DMA source offsets within a chunk (fixed for the sequence).
+  uint32_t koff[C::kKDma], uoff[C::kUDma];
+#pragma unroll
+  for (int i = 0; i < C::kKDma; ++i) {
+    const int P = (wi * C::kKDma + i) * 64 + lane;
+    koff[i] = (uint32_t)(hl::dma_row(P, C::kRowK) * tsk + hl::dma_chunk(P, C::kRowK) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < C::kUDma; ++i) {
+    const int P = (wi * C::kUDma + i) * 64 + lane;
+    uoff[i] = (uint32_t)(hl::dma_row(P, C::kRowU) * tsv + hl::dma_chunk(P, C::kRowU) * 16);
+  }
+  const uint32_t goff = (uint32_t)(lane * H * 4);
+
+  auto issue = [&](int64_t cc, int s) {
+    const char* kb = reinterpret_cast<const char*>(k) + kc0 + cc * kcs;
+    const uint32_t lk = lds_address(stage_k(s)) + wi * C::kKDma * 1024;
+#pragma unroll
+    for (int i = 0; i < C::kKDma; ++i) dma_b128(kb, koff[i], __builtin_amdgcn_readfirstlane(lk + i * 1024));
+    if constexpr (DELTA) {
+      const char* wb = reinterpret_cast<const char*>(w) + kc0 + cc * kcs;
+      const uint32_t lw = lds_address(stage_w(s)) + wi * C::kKDma * 1024;
+#pragma unroll
+      for (int i = 0; i < C::kKDma; ++i) dma_b128(wb, koff[i], __builtin_amdgcn_readfirstlane(lw + i * 1024));
+    }
+    const char* ub = reinterpret_cast<const char*>(vu) + uc0 + cc * ucs;
+    const uint32_t lu = lds_address(stage_u(s)) + wi * C::kUDma * 1024;
+#pragma unroll
+    for (int i = 0; i < C::kUDma; ++i) dma_b128(ub, uoff[i], __builtin_amdgcn_readfirstlane(lu + i * 1024));
+    if constexpr (HAS_G) {
+      const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
+      dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s)) + wi * 256));
+    }
+  };
+
+  // State S[kappa = kap0 + 16 kb + 4 grp + r][n = v0 + 16 wq + li] in S[kb][r].
+  f32x4 S[C::KBH];
+  const int ncol = v0 + 16 * wq + li;
+  const int64_t st_base = bh * (int64_t)(K * V);
+#pragma unroll
+  for (int kb = 0; kb < C::KBH; ++kb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[kb][r] = h0 ? h0[st_base + (int64_t)(kap0 + 16 * kb + 4 * grp + r) * V + ncol] : 0.f;
+  // Retire the h0 loads here: a load still pending at the loop entry would
+  // make the compiler wait for every outstanding operation inside the loop.
+  wait_vmcnt<0>();
+
+  // Store offsets after the quad transpose: lane (grp, 4 m4 + qq) holds row
+  // 4 grp + qq of a 16-row tile at columns 16 wq + 4 m4 .. + 3.
+  const int m4 = li >> 2, qq = li & 3;
+  const uint32_t hoff0 = (uint32_t)(((kap0 + 4 * grp + qq) * V + v0 + 16 * wq + 4 * m4) * 4);
+  const uint32_t vnoff0 = (uint32_t)((4 * grp + qq) * tsv + (v0 + 16 * wq + 4 * m4) * 2);
+  auto store_h = [&](int64_t c) {
+    float* hb = hout + ((b * NT + c) * H + hh) * (int64_t)(K * V);
+#pragma unroll
+    for (int kb = 0; kb < C::KBH; ++kb)
+      st_b128(hb, hoff0 + (uint32_t)(kb * 16 * V * 4), __builtin_bit_cast(u32x4, quad_transpose(S[kb])));
+  };
+
+  if (NT > 0) {
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i) issue(i < NT ? i : NT - 1, i);
+  }
+  for (int64_t c = 0; c < NT; ++c) {
+    const int s = (int)(c % NS);
+    if (c < NS - 1) wait_vmcnt<C::kWaitFirst>();
+    else wait_vmcnt<C::kWaitSteady>();
+    lds_barrier();  // A: chunk c is in LDS; every wave is done with chunk c - 1
+    {
+      const int64_t cn = c + NS - 1;
+      issue(cn < NT ? cn : NT - 1, (int)(cn % NS));
+    }
+    if constexpr (DELTA) store_h(c);  // state before chunk c
+
+    const char* tk = stage_k(s);
+    const char* tu = stage_u(s);
+    // v (or u) rows j = 16 jb + 4 grp + r of column 16 wq + li.
+    f32x4 vn[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(
+          tu + hl::tile_off(16 * jb + 4 * grp + (li >> 2), 16 * wq + 4 * (li & 3), C::kRowU)));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
+    }
+
+    if constexpr (DELTA) {
+      const char* tw = stage_w(s);
+      bf16x8 sb[C::KBH / 2];
+#pragma unroll
+      for (int s2 = 0; s2 < C::KBH / 2; ++s2) {
+        const float f[8] = {S[2 * s2][0], S[2 * s2][1], S[2 * s2][2], S[2 * s2][3],
+                            S[2 * s2 + 1][0], S[2 * s2 + 1][1], S[2 * s2 + 1][2], S[2 * s2 + 1][3]};
+        sb[s2] = to_bf16x8(f);
+      }
+      f32x4 part[4];
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb) {
+        f32x4 acc = zero4();
+        const int row = 16 * jb + li;
+#pragma unroll
+        for (int s2 = 0; s2 < C::KBH / 2; ++s2) {
+          const int e0 = kap0 + 32 * s2 + 4 * grp;
+          const bf16x4 a0 = *reinterpret_cast<const bf16x4*>(tw + hl::tile_off(row, e0, C::kRowK));
+          const bf16x4 a1 = *reinterpret_cast<const bf16x4*>(tw + hl::tile_off(row, e0 + 16, C::kRowK));
+          acc = mfma16x16x32(concat(a0, a1), sb[s2], acc);
+        }
+        part[jb] = acc;
+        if constexpr (KS == 2) *reinterpret_cast<f32x4*>(xbuf + ((wi * 4 + jb) * 64 + lane) * 4) = acc;
+      }
+      if constexpr (KS == 2) {
+        lds_barrier();  // B: both K halves' partials are in LDS
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          const f32x4 o = *reinterpret_cast<const f32x4*>(xbuf + (((wi ^ 4) * 4 + jb) * 64 + lane) * 4);
+          vn[jb] -= part[jb] + o;
+        }
+      } else {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) vn[jb] -= part[jb];
+      }
+      if constexpr (STORE_VN) {
+        bf16* vb = vnew + ((b * T + c * kBT) * H + hh) * V;
+#pragma unroll
+        for (int jj = 0; jj < C::kJbStore; ++jj) {
+          const int jb = C::kJbStore * kh + jj;
+          const f32x4 t = quad_transpose(vn[jb]);
+          bf16x4 o;
+          o[0] = (bf16)t[0]; o[1] = (bf16)t[1]; o[2] = (bf16)t[2]; o[3] = (bf16)t[3];
+          st_b64(vb, vnoff0 + (uint32_t)(16 * jb * tsv), __builtin_bit_cast(u32x2, o));
+        }
+      }
+    }
+
+    // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
+    bf16x8 vh[2];
+    float decay = 1.f;
+    if constexpr (HAS_G) {
+      const float* gs = stage_g(s) + wi * kBT;
+      const float gl = gs[kBT - 1];
+      decay = fast_exp(gl);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        float f[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j0 = 32 * s2 + 4 * grp + r;
+          f[r] = vn[2 * s2][r] * fast_exp(gl - gs[j0]);
+          f[4 + r] = vn[2 * s2 + 1][r] * fast_exp(gl - gs[j0 + 16]);
+        }
+        vh[s2] = to_bf16x8(f);
+      }
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const float f[8] = {vn[2 * s2][0], vn[2 * s2][1], vn[2 * s2][2], vn[2 * s2][3],
+                            vn[2 * s2 + 1][0], vn[2 * s2 + 1][1], vn[2 * s2 + 1][2], vn[2 * s2 + 1][3]};
+        vh[s2] = to_bf16x8(f);
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < C::KBH; ++kb) {
+      if constexpr (HAS_G) S[kb] *= decay;
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int col = kap0 + 16 * kb + 4 * (li & 3);
+        const bf16x4 a = ds_read_tr16(reinterpret_cast<const bf16*>(
+            tk + hl::tile_off(32 * s2 + 4 * grp + (li >> 2), col, C::kRowK)));
+        const bf16x4 bq = ds_read_tr16(reinterpret_cast<const bf16*>(
+            tk + hl::tile_off(32 * s2 + 16 + 4 * grp + (li >> 2), col, C::kRowK)));
+        S[kb] = mfma16x16x32(concat(a, bq), vh[s2], S[kb]);
+      }
+    }
+    if constexpr (!DELTA) store_h(c);  // state after chunk c
+  }
+  // Drain: no DMA may still target this workgroup's LDS when it exits.
+  wait_vmcnt<0>();
+
+  if (ht) {
+#pragma unroll
+    for (int kb = 0; kb < C::KBH; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        ht[st_base + (int64_t)(kap0 + 16 * kb + 4 * grp + r) * V + ncol] = S[kb][r];
+  }
+}
+
+// Measured on MI355X at B=8, T=8192, H=16, K=V=128 (256 workgroups): the K
+// split with a 2-stage ring is the fastest form (3 stages and the unsplit form
+// are slower); every form is bound by HBM traffic, 2.16 GB per launch.
+constexpr int kHKSplit = 2;  // K split of the bf16 pipeline
+constexpr int kHStages = 2;  // DMA ring depth of the bf16 pipeline
+// The DMA pipeline serves grids that fill the GPU (bandwidth-bound); below
+// that, fewer and serial chunks are latency-bound and the register-prefetch
+// kernel (shorter chunk-to-chunk latency) is faster.
+constexpr int64_t kHDmaMinGrid = 256;
+
+template <int K, int V, bool DELTA>
+hipError_t launch_h_dma(const void* k, const void* w, const void* vu, const void* g, const void* h0,
+                        void* h, void* vnew, void* ht, int64_t B, int64_t T, int64_t H, hipStream_t s) {
+  const int64_t NT = T / kBT;
+  const int64_t BH = B * H;
+  const dim3 grid((unsigned)(BH * (V / kHBV)));
+  constexpr int KS = kHKSplit, NS = kHStages;
+#define THM_H_DMA_LAUNCH(HG, SV)                                                               \
+  hipLaunchKernelGGL((chunk_fwd_h_dma_kernel<K, V, KS, NS, DELTA, HG, SV>), grid,              \
+                     dim3(PCfg<K, KS, NS, DELTA, HG, SV>::kThreads), 0, s, (const bf16*)k,     \
+                     (const bf16*)w, (const bf16*)vu, (const float*)g, (const float*)h0,       \
+                     (float*)h, (bf16*)vnew, (float*)ht, T, H, NT, BH)
+  const bool sv = DELTA && vnew != nullptr;
+  if (g) {
+    if (sv) THM_H_DMA_LAUNCH(true, DELTA);
+    else THM_H_DMA_LAUNCH(true, false);
+  } else {
+    if (sv) THM_H_DMA_LAUNCH(false, DELTA);
+    else THM_H_DMA_LAUNCH(false, false);
+  }
+#undef THM_H_DMA_LAUNCH
+  return hipGetLastError();
+}
+
 template <typename IT, int K, int V, bool DELTA>
 hipError_t launch_h(const void* k, const void* w, const void* vu, const void* g, const void* h0,
                     void* h, void* vnew, void* ht, int64_t B, int64_t T, int64_t H, hipStream_t s) {
@@ -342,14 +664,24 @@ hipError_t launch_h(const void* k, const void* w, const void* vu, const void* g,
   return hipGetLastError();
 }
 
+template <typename IT, bool DELTA, int K, int V>
+hipError_t launch_kv(const void* k, const void* w, const void* vu, const void* g, const void* h0,
+                     void* h, void* vnew, void* ht, int64_t B, int64_t T, int64_t H, hipStream_t s) {
+  if constexpr (std::is_same<IT, bf16>::value) {
+    if (B * H * (V / kHBV) >= kHDmaMinGrid)
+      return launch_h_dma<K, V, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+  }
+  return launch_h<IT, K, V, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+}
+
 template <typename IT, bool DELTA>
 hipError_t dispatch_kv(int64_t K, int64_t V, const void* k, const void* w, const void* vu,
                        const void* g, const void* h0, void* h, void* vnew, void* ht, int64_t B,
                        int64_t T, int64_t H, hipStream_t s) {
-  if (K == 64 && V == 64) return launch_h<IT, 64, 64, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
-  if (K == 64 && V == 128) return launch_h<IT, 64, 128, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
-  if (K == 128 && V == 64) return launch_h<IT, 128, 64, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
-  return launch_h<IT, 128, 128, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+  if (K == 64 && V == 64) return launch_kv<IT, DELTA, 64, 64>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+  if (K == 64 && V == 128) return launch_kv<IT, DELTA, 64, 128>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+  if (K == 128 && V == 64) return launch_kv<IT, DELTA, 128, 64>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+  return launch_kv<IT, DELTA, 128, 128>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
 }
 
 }  // namespace

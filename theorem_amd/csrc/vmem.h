@@ -1,0 +1,106 @@
+// Vector-memory instructions issued by hand, for pipelines whose waits are
+// counted by hand (gfx950).
+//
+// The compiler's automatic wait insertion treats every LDS read after a
+// global -> LDS DMA as dependent on it and waits for all outstanding vector
+// memory operations (vmcnt(0)), which serialises a multi-stage LDS ring.  The
+// kernels that use these helpers therefore issue their DMA loads and their
+// global stores here, in inline assembly the compiler does not track, and
+// wait with an explicit vmcnt(N): loads and stores retire in issue order on
+// one counter, so once at most N operations are outstanding, every operation
+// issued before the last N has completed.
+//
+// All operands named `base` and `lds` must be wave-uniform; `voff` is a
+// per-lane 32-bit byte offset from `base`.
+#pragma once
+
+#include "common.h"
+
+namespace thm {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 32-bit LDS address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(size_t)(lds_void_t*)p;
+}
+
+// global -> LDS, 16 bytes per lane: lane i's bytes [base + voff_i, +16) land at
+// LDS [lds + 16 i, +16).  M0 (the LDS base register) is restored afterwards.
+__device__ __forceinline__ void dma_b128(const void* base, uint32_t voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(base), "s"(lds)
+      : "memory");
+}
+
+// global -> LDS, 4 bytes per lane: lane i's bytes [base + voff_i, +4) land at
+// LDS [lds + 4 i, +4).
+__device__ __forceinline__ void dma_b32(const void* base, uint32_t voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(base), "s"(lds)
+      : "memory");
+}
+
+// Vector global stores of 16 / 8 bytes per lane at base + voff.  A store of
+// more than 8 bytes reads its upper data registers a cycle after issue, and a
+// VALU write to them must wait for that; the compiler inserts that wait for the
+// stores it emits but not after inline assembly, so the wait states are part of
+// the statement.
+__device__ __forceinline__ void st_b128(void* base, uint32_t voff, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, %2\n\ts_nop 1" : : "v"(voff), "v"(v), "s"(base) : "memory");
+}
+__device__ __forceinline__ void st_b64(void* base, uint32_t voff, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, %2" : : "v"(voff), "v"(v), "s"(base) : "memory");
+}
+
+// Wait until at most N vector memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Transpose the 4x4 matrix held by each quad of lanes (lane 4m + q holds row q
+// in v[0..3]): afterwards lane 4m + q holds column q, i.e. r[i] = the v[q] of
+// lane 4m + i.  Two DPP butterfly steps (quad_perm xor 1, xor 2).
+__device__ __forceinline__ float dpp_quad_xor1(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_quad_xor2(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ f32x4 quad_transpose(f32x4 v) {
+  const int q = lane_id() & 3;
+  const bool q0 = q & 1, q1 = q & 2;
+  const float x0 = dpp_quad_xor1(v[1]), x1 = dpp_quad_xor1(v[0]);
+  const float x2 = dpp_quad_xor1(v[3]), x3 = dpp_quad_xor1(v[2]);
+  f32x4 a;
+  a[0] = q0 ? x0 : v[0];
+  a[1] = q0 ? v[1] : x1;
+  a[2] = q0 ? x2 : v[2];
+  a[3] = q0 ? v[3] : x3;
+  const float y0 = dpp_quad_xor2(a[2]), y1 = dpp_quad_xor2(a[3]);
+  const float y2 = dpp_quad_xor2(a[0]), y3 = dpp_quad_xor2(a[1]);
+  f32x4 r;
+  r[0] = q1 ? y0 : a[0];
+  r[1] = q1 ? y1 : a[1];
+  r[2] = q1 ? a[2] : y2;
+  r[3] = q1 ? a[3] : y3;
+  return r;
+}
+
+}  // namespace thm
