@@ -46,6 +46,10 @@ extern "C" {
 #define THM_ACT_NONE 0 /* the reference's behaviour (no activation)          */
 #define THM_ACT_SILU 1 /* x * sigmoid(x); extension, not in the reference    */
 
+/* Gate transforms for thm_chunk_local_cumsum. */
+#define THM_GATE_IDENTITY 0   /* g = chunk-local cumsum of a              */
+#define THM_GATE_LOGSIGMOID 1 /* g = chunk-local cumsum of log(sigmoid(a)) */
+
 /* Flags for thm_chunk_fwd_h. */
 #define THM_H_DELTA 1 /* delta-rule form: v_new = u - w.S, h[c] stored BEFORE the
                          update of chunk c, optional v_new / final-state output.
@@ -127,6 +131,36 @@ int thm_chunk_fwd_o(const void* q, const void* k, const void* v, const void* g,
                     const void* h, void* o, float scale,
                     int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
                     int32_t chunk_size, int32_t qkv_dtype, void* stream);
+
+/*
+ * WY matrix of the chunked Gated DeltaNet forward, per chunk c of
+ * chunk_size = 64 tokens:
+ *   M[i][j] = beta_i (k_i . k_j) exp(g_i - g_j) for j < i (0 on and above the diagonal),
+ *   A_c = (I + sign M)^{-1}
+ * with A_c[r, :] stored at A[b, c*64 + r, h, :] (the layout recompute_w_u reads).
+ * sign = -1 is the reference's (I - M)^{-1}: replaces `_build_A` of
+ * kernels/recompute_w_u/reference.py:48-91 (torch matmul + solve_triangular);
+ * sign = +1 is the gated delta rule's (I + M)^{-1}.
+ *   k_dtype: dtype of k (F32 or BF16). beta, g and A are fp32.
+ *   g may be NULL (no gate). K in {64, 128}; T % 64 == 0.
+ */
+int thm_wy_build_A(const void* k, const void* beta, const void* g, void* A,
+                   int64_t B, int64_t T, int64_t H, int64_t K,
+                   int32_t chunk_size, int32_t k_dtype, int32_t sign, void* stream);
+
+/*
+ * Gate preprocessing: per 64-token chunk, the inclusive cumulative sum of the
+ * per-token log decay,
+ *   g[b, t, h] = sum_{t' in chunk(t), t' <= t} f(a[b, t', h]),
+ * f = identity (THM_GATE_IDENTITY) or log(sigmoid(.)) (THM_GATE_LOGSIGMOID).
+ * This is the chunk-local cumulative gate g that every chunk kernel above
+ * takes; the reference forms it inside its input generators
+ * (kernels/chunk_fwd_h/reference.py:15-47, kernels/recompute_w_u/reference.py:94-115,
+ * `reshape(B, T/BT, BT, H).cumsum(dim=2)`).
+ *   a_dtype: dtype of a (F32 or BF16); g is fp32 [B, T, H]. T % 64 == 0.
+ */
+int thm_chunk_local_cumsum(const void* a, void* g, int64_t B, int64_t T, int64_t H,
+                           int32_t chunk_size, int32_t a_dtype, int32_t mode, void* stream);
 
 #ifdef __cplusplus
 }

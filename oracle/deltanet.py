@@ -36,6 +36,12 @@ def chunk_local_cumsum(a: np.ndarray, bt: int = BT) -> np.ndarray:
     return np.cumsum(a.reshape(B, T // bt, bt, H), axis=2).reshape(B, T, H)
 
 
+def logsigmoid(x: np.ndarray) -> np.ndarray:
+    """log(sigmoid(x)) = min(x, 0) - log1p(exp(-|x|)) (the logsigmoid gate of the
+    gated delta rule; the reference's generators use plain negative increments)."""
+    return np.minimum(x, 0.0) - np.log1p(np.exp(-np.abs(x)))
+
+
 # --------------------------------------------------------------------------- chunk_fwd_h
 
 def chunk_fwd_h_ref(k, v, g, bt: int = BT, dtype=np.float64) -> np.ndarray:

@@ -25,7 +25,8 @@ def declared_symbols() -> list[str]:
 def test_header_lists_entry_points():
     syms = declared_symbols()
     assert {"thm_causal_conv1d_fwd", "thm_recompute_w_u_fwd", "thm_chunk_fwd_h",
-            "thm_chunk_fwd_o", "thm_status_string", "thm_abi_version"} <= set(syms)
+            "thm_chunk_fwd_o", "thm_wy_build_A", "thm_chunk_local_cumsum",
+            "thm_status_string", "thm_abi_version"} <= set(syms)
 
 
 def test_library_exports_every_declared_symbol():
@@ -70,3 +71,30 @@ def test_python_wrapper_rejects_cpu_tensors():
     x = torch.zeros(1, 4, 8)
     with pytest.raises(AssertionError):
         custom_kernel((x, torch.zeros(4, 3), torch.zeros(4)))
+
+
+def test_build_A_and_cumsum_validation():
+    lib = _capi.load_library()
+
+    def A(**kw):
+        a = dict(k=FAKE, beta=FAKE, g=FAKE, A=FAKE, B=1, T=64, H=2, K=64, bt=64, kd=1, sign=1)
+        a.update(kw)
+        return lib.thm_wy_build_A(a["k"], a["beta"], a["g"], a["A"], a["B"], a["T"], a["H"], a["K"],
+                                  a["bt"], a["kd"], a["sign"], None)
+
+    assert A(k=None) == -1 and A(beta=None) == -1 and A(A=None) == -1
+    assert A(T=65) == -2 and A(H=0) == -2 and A(B=-1) == -2
+    assert A(kd=5) == -3 and A(K=96) == -4 and A(bt=32) == -6 and A(sign=0) == -6
+    assert A(k=FAKE + 8) == -5 and A(beta=FAKE + 2) == -5
+    assert A(B=0) == 0 and A(T=0) == 0
+
+    def cs(**kw):
+        a = dict(a=FAKE, g=FAKE, B=1, T=64, H=2, bt=64, ad=0, mode=0)
+        a.update(kw)
+        return lib.thm_chunk_local_cumsum(a["a"], a["g"], a["B"], a["T"], a["H"], a["bt"], a["ad"], a["mode"], None)
+
+    assert cs(a=None) == -1 and cs(g=None) == -1
+    assert cs(T=100) == -2 and cs(H=0) == -2
+    assert cs(ad=3) == -3 and cs(mode=2) == -6 and cs(bt=128) == -6
+    assert cs(g=FAKE + 2) == -5 and cs(a=FAKE + 1, ad=1) == -5
+    assert cs(B=0) == 0

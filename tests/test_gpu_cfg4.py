@@ -105,6 +105,16 @@ def test_cfg4_chain_matches_token_recurrence(chain):
         assert_close(d["ht"][b:b + 1, hh:hh + 1], eS, 1e-2, 1e-2, f"chain final state (b={b}, head={hh})")
 
 
+def test_cfg4_build_A_full(chain):
+    # The HIP WY matrix over all 16384 chunks against the A of the input
+    # generator (built per chunk in float64 on the GPU, then rounded to fp32).
+    d = chain
+    A = recompute_w_u.build_A(d["k"], d["beta"], d["g"], sign=+1)
+    torch.cuda.synchronize()
+    dev = float((A - d["A"]).abs().max())
+    assert dev <= 1e-4 * float(d["A"].abs().max()), f"A max |diff| {dev:.3e}"
+
+
 def test_cfg4_homogeneity(chain):
     # w, u are linear in A; h, v_new, final state are linear in u (zero initial
     # state); o is linear in (v, h) jointly.

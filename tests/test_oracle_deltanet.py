@@ -290,3 +290,36 @@ def test_mutations_are_caught():
     o_bad = dn.chunk_fwd_o_diff(q, kn, vn, g2, hh, 0.25)
     eo, _ = dn.gated_delta_rule_tokens(q, kn, v, beta, a, 0.25)
     assert np.abs(o_bad - eo).max() > 1e-3
+
+
+# --------------------------------------------------------------------------- gates
+
+def test_chunk_local_cumsum_pins():
+    # Brute-force loop; constant increment closed form a * (t % 64 + 1); the
+    # sum restarts at every chunk; first differences inside a chunk give a back.
+    a = rand(2, 192, 3)
+    g = dn.chunk_local_cumsum(a)
+    ref = np.zeros_like(a)
+    for b in range(2):
+        for h in range(3):
+            run = 0.0
+            for t in range(192):
+                run = a[b, t, h] if t % 64 == 0 else run + a[b, t, h]
+                ref[b, t, h] = run
+    np.testing.assert_allclose(g, ref, rtol=1e-12, atol=1e-12)
+    c = dn.chunk_local_cumsum(np.full((1, 128, 1), -0.25))
+    np.testing.assert_allclose(c[0, :, 0], -0.25 * (np.arange(128) % 64 + 1))
+    assert np.all(g[:, ::64] == a[:, ::64])
+    d = np.diff(g.reshape(2, 3, 64, 3), axis=2)
+    np.testing.assert_allclose(d, a.reshape(2, 3, 64, 3)[:, :, 1:], atol=1e-12)
+
+
+def test_logsigmoid_pins():
+    # torch's library routine, logsigmoid(0) = -log 2, the tails (-> 0 and -> x),
+    # and logsigmoid(x) - logsigmoid(-x) = x.
+    x = np.linspace(-60, 60, 4001)
+    np.testing.assert_allclose(dn.logsigmoid(x), torch.nn.functional.logsigmoid(torch.from_numpy(x)).numpy(),
+                               rtol=1e-12, atol=1e-12)
+    assert abs(dn.logsigmoid(np.array([0.0]))[0] + np.log(2.0)) < 1e-15
+    np.testing.assert_allclose(dn.logsigmoid(np.array([50.0, -50.0])), [0.0, -50.0], atol=1e-15)
+    np.testing.assert_allclose(dn.logsigmoid(x) - dn.logsigmoid(-x), x, atol=1e-12)

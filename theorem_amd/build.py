@@ -27,6 +27,8 @@ SOURCES = [
     "recompute_w_u.hip",
     "chunk_fwd_h.hip",
     "chunk_fwd_o.hip",
+    "wy_build_A.hip",
+    "gates.hip",
 ]
 
 ARCH = "gfx950"

@@ -11,40 +11,52 @@ it reproduces the token-by-token gated delta rule
     S_t = e^{a_t} S_{t-1};  S_t += beta_t k_t (v_t - S_t^T k_t)^T;  o_t = scale S_t^T q_t
 with g the chunk-local cumsum of a.
 
-``build_A`` is not one of the four kernels: it runs as batched torch ops on
-the GPU (fp32 matmul + unit-triangular solve).
+``build_A`` (the WY matrix) is the HIP kernel thm_wy_build_A.
 """
 from __future__ import annotations
 
 import torch
 
-from .kernels import chunk_fwd_h, chunk_fwd_o, recompute_w_u
+from .kernels import _capi, chunk_fwd_h, chunk_fwd_o, recompute_w_u
 
 BT = 64
 
 
+def chunk_local_cumsum(a: torch.Tensor, logsigmoid: bool = False) -> torch.Tensor:
+    """g [B, T, H] fp32: per 64-token chunk, the inclusive cumsum of a (or of
+    log(sigmoid(a)) with ``logsigmoid``), on the GPU (thm_chunk_local_cumsum)."""
+    B, T, H = a.shape
+    assert T % BT == 0, f"T={T} must be a multiple of {BT}"
+    _capi.require_device(a)
+    code = _capi.dtype_code(a, "a")
+    a = _capi.prep(a, "a")
+    g = torch.empty(B, T, H, dtype=torch.float32, device=a.device)
+    status = _capi.load_library().thm_chunk_local_cumsum(
+        _capi.ptr(a), _capi.ptr(g), B, T, H, BT, code, 1 if logsigmoid else 0, _capi.stream_of(a))
+    _capi.check(status, "thm_chunk_local_cumsum")
+    return g
+
+
 def build_A(k: torch.Tensor, beta: torch.Tensor, g: torch.Tensor | None) -> torch.Tensor:
-    """A [B, T, H, 64] fp32 = per-chunk (I + strict_lower(beta_i k_i.k_j e^{g_i - g_j}))^{-1}."""
-    B, T, H, K = k.shape
-    n = T // BT
-    kc = k.float().reshape(B, n, BT, H, K).permute(0, 1, 3, 2, 4).contiguous()
-    bc = beta.float().reshape(B, n, BT, H).permute(0, 1, 3, 2)
-    M = (kc @ kc.transpose(-1, -2).contiguous()) * bc.unsqueeze(-1)
-    if g is not None:
-        gc = g.float().reshape(B, n, BT, H).permute(0, 1, 3, 2)
-        M = M * torch.exp(gc.unsqueeze(-1) - gc.unsqueeze(-2))
-    M = torch.tril(M, diagonal=-1)
-    eye = torch.eye(BT, device=k.device, dtype=torch.float32).expand_as(M)
-    Ac = torch.linalg.solve_triangular(eye + M, eye, upper=False, unitriangular=True)
-    return Ac.permute(0, 1, 3, 2, 4).reshape(B, T, H, BT).contiguous()
+    """A [B, T, H, 64] fp32 = per-chunk (I + strict_lower(beta_i k_i.k_j e^{g_i - g_j}))^{-1} (HIP)."""
+    return recompute_w_u.build_A(k, beta, g, sign=+1)
 
 
 def chunk_gated_delta_rule_fwd(q, k, v, beta, g, scale: float, initial_state=None,
                                output_final_state: bool = False, A: torch.Tensor | None = None,
-                               return_intermediates: bool = False):
-    """o [B, T, H, V] (dtype of q) and the final state [B, H, K, V] fp32 (or None)."""
+                               return_intermediates: bool = False, a: torch.Tensor | None = None,
+                               a_logsigmoid: bool = False):
+    """o [B, T, H, V] (dtype of q) and the final state [B, H, K, V] fp32 (or None).
+
+    ``g`` is the chunk-local cumulative log decay [B, T, H] fp32 (or None: no
+    gate).  Alternatively pass the per-token log decay ``a`` (g = None): g is
+    then formed on the GPU by chunk_local_cumsum(a), of log(sigmoid(a)) when
+    ``a_logsigmoid``."""
     B, T, H, K = k.shape
     V = v.shape[-1]
+    if a is not None:
+        assert g is None, "pass either g or a"
+        g = chunk_local_cumsum(a, logsigmoid=a_logsigmoid)
     if A is None:
         A = build_A(k, beta, g)
     w, u = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V))
@@ -52,5 +64,5 @@ def chunk_gated_delta_rule_fwd(q, k, v, beta, g, scale: float, initial_state=Non
                                                   output_final_state=output_final_state))
     o = chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=v_new, g=g, h=h, scale=scale))
     if return_intermediates:
-        return o, ht, dict(A=A, w=w, u=u, h=h, v_new=v_new)
+        return o, ht, dict(A=A, g=g, w=w, u=u, h=h, v_new=v_new)
     return o, ht
