@@ -79,6 +79,36 @@ int thm_causal_conv1d_fwd(const void* x, const void* weight, const void* bias, v
                           void* stream);
 
 /*
+ * Channels-last variant of thm_causal_conv1d_fwd: x, out [batch, seqlen, dim]
+ * with dim contiguous (in PyTorch terms, a [batch, dim, seqlen] tensor that is
+ * a transposed view of a contiguous [batch, seqlen, dim] one).  Same math,
+ * arguments and status codes as thm_causal_conv1d_fwd.  No counterpart in the
+ * reference, whose conv asserts the [batch, dim, seqlen] layout
+ * (kernels/causal_conv1d/kernel.py:184); this is the layout a Mamba-2 block
+ * holds its activations in.
+ */
+int thm_causal_conv1d_fwd_channels_last(const void* x, const void* weight, const void* bias,
+                                        void* out, int64_t batch, int64_t seqlen, int64_t dim,
+                                        int32_t width, int32_t x_dtype, int32_t w_dtype,
+                                        int32_t activation, void* stream);
+
+/*
+ * Decode step of the causal conv with a rolling state, per (b, d):
+ *   window = conv_state[b, d, 0..state_len) ++ x[b, d, 0..seqlen)
+ *   out[b, d, t] = act( bias[d] + sum_{k<width} weight[d,k] * window[state_len - width + 1 + t + k] )
+ *   conv_state[b, d, :] = the last state_len samples of window   (updated in place)
+ * x, out [batch, dim, seqlen]; conv_state [batch, dim, state_len] in x_dtype,
+ * state_len >= width - 1.  Running it token by token from a zero state gives
+ * thm_causal_conv1d_fwd of the whole sequence.  No counterpart in the
+ * reference (which has no decode path); it is the incremental form of the
+ * reference's conv (kernels/causal_conv1d/reference.py:55-81).
+ */
+int thm_causal_conv1d_update(const void* x, void* conv_state, const void* weight, const void* bias,
+                             void* out, int64_t batch, int64_t dim, int64_t seqlen,
+                             int64_t state_len, int32_t width, int32_t x_dtype, int32_t w_dtype,
+                             int32_t activation, void* stream);
+
+/*
  * Gated DeltaNet WY recompute, per chunk c of chunk_size = 64 tokens:
  *   w_c = A_c . (k_c * (beta_c * exp(g_c)))      [64 x K]
  *   u_c = A_c . (v_c * beta_c)                   [64 x V]

@@ -82,3 +82,20 @@ def causal_conv1d_bruteforce(x: np.ndarray, weight: np.ndarray, bias: np.ndarray
 
 def silu(x: np.ndarray) -> np.ndarray:
     return x / (1.0 + np.exp(-x))
+
+
+def causal_conv1d_update_ref(x: np.ndarray, state: np.ndarray, weight: np.ndarray, bias: np.ndarray | None,
+                             dtype=np.float64):
+    """Decode step with a rolling state, restated from the conv's definition
+    (scripts/cpu_reference.py:40-63 applied to the window state ++ x):
+        window = state ++ x (along time),  out[t] = bias + sum_k w[k] window[L_s - W + 1 + t + k],
+        new state = the last L_s samples of window.
+    x [B, D, L], state [B, D, L_s].  Returns (out [B, D, L], new state)."""
+    B, D, L = x.shape
+    Ls = state.shape[2]
+    W = weight.shape[1]
+    win = np.concatenate([state.astype(dtype), x.astype(dtype)], axis=2)
+    out = np.zeros((B, D, L), dtype=dtype) + (0 if bias is None else bias.astype(dtype)[None, :, None])
+    for k in range(W):
+        out += weight.astype(dtype)[None, :, k, None] * win[:, :, Ls - W + 1 + k:Ls - W + 1 + k + L]
+    return out, win[:, :, L:]

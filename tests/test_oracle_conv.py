@@ -94,3 +94,28 @@ def test_silu_pins():
     assert conv.silu(np.array([0.0]))[0] == 0.0
     np.testing.assert_allclose(conv.silu(np.array([40.0, -40.0])), [40.0, 0.0], atol=1e-12)
     np.testing.assert_allclose(got - conv.silu(-x), x, atol=1e-12)
+
+
+def test_update_ref_pins():
+    # Token-by-token decode from a zero state reproduces the full-sequence conv
+    # (the NumPy restatement), the state is the last L_s samples, and a chunked
+    # decode (L > 1) equals the token-by-token one.
+    rng = np.random.default_rng(5)
+    for W, Ls in ((4, 3), (4, 6), (1, 0), (3, 2)):
+        x = rng.standard_normal((2, 3, 20))
+        w = rng.standard_normal((3, W))
+        b = rng.standard_normal(3)
+        full = conv.causal_conv1d_numpy(x, w, b, dtype=np.float64)
+        st = np.zeros((2, 3, Ls))
+        outs = []
+        for t in range(20):
+            o, st = conv.causal_conv1d_update_ref(x[:, :, t:t + 1], st, w, b)
+            outs.append(o)
+        np.testing.assert_allclose(np.concatenate(outs, axis=2), full, rtol=1e-12, atol=1e-12)
+        if Ls:
+            np.testing.assert_array_equal(st, x[:, :, 20 - Ls:])
+        st2 = np.zeros((2, 3, Ls))
+        o1, st2 = conv.causal_conv1d_update_ref(x[:, :, :7], st2, w, b)
+        o2, st2 = conv.causal_conv1d_update_ref(x[:, :, 7:], st2, w, b)
+        np.testing.assert_allclose(np.concatenate([o1, o2], axis=2), full, rtol=1e-12, atol=1e-12)
+        np.testing.assert_array_equal(st2, st)

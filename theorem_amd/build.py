@@ -24,6 +24,7 @@ LIB_PATH = LIB_DIR / LIB_NAME
 SOURCES = [
     "capi.cpp",
     "causal_conv1d.hip",
+    "causal_conv1d_ext.hip",
     "recompute_w_u.hip",
     "chunk_fwd_h.hip",
     "chunk_fwd_o.hip",

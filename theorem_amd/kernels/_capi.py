@@ -35,6 +35,10 @@ SIGNATURES = {
     "thm_status_string": [ctypes.c_int],
     "thm_causal_conv1d_fwd": [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i32,
                               _c_i32, _c_i32, _c_i32, _c_vp],
+    "thm_causal_conv1d_fwd_channels_last": [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                            _c_i32, _c_i32, _c_i32, _c_i32, _c_vp],
+    "thm_causal_conv1d_update": [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                                 _c_i32, _c_i32, _c_i32, _c_i32, _c_vp],
     "thm_recompute_w_u_fwd": [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                               _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_vp],
     "thm_chunk_fwd_h": [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
