@@ -103,6 +103,21 @@ def test_o_config_inputs(dev, K, V, dtype, gate):
     assert_close(o, e, tol, tol, f"o K={K} V={V} {dtype} {gate}")
 
 
+# bf16 grids with at least 2 tiles per persistent workgroup (2 per CU) run the
+# software-pipelined kernel; these shapes (1024+ tiles) force it at every K, V.
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("gate", ["logsigmoid", None])
+def test_o_pipelined_path(dev, K, V, gate):
+    B, T, H = 2, 2048, 17
+    d = configs.make_o_inputs(B, T, H, K, V, seed=13, device=dev, dtype=torch.bfloat16, gate=gate or "zero")
+    g = d["g"] if gate else None
+    o = chunk_fwd_o.custom_kernel(dict(q=d["q"], k=d["k"], v=d["v"], g=g, h=d["h"], scale=d["scale"]))
+    sync()
+    e = odn.chunk_fwd_o_diff(np_(d["q"]), np_(d["k"]), np_(d["v"]), np_(g) if g is not None else None,
+                             np_(d["h"]), d["scale"])
+    assert_close(o, e, 1e-2, 1e-2, f"o K={K} V={V} gate={gate}")
+
+
 def test_o_closed_forms(dev):
     d = configs.make_o_inputs(1, 128, 2, 64, 64, seed=4, device=dev, dtype=torch.float32)
     q, k, v, h = d["q"], d["k"], d["v"], d["h"]

@@ -237,6 +237,194 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
   for (int nb = 0; nb < NB; ++nb) store4(o + qrow * V + 16 * nb + 4 * grp, acc[nb] * scale);
 }
 
+// ---------------------------------------------------------------------------
+// bf16 inputs on grids larger than the GPU: persistent, software-pipelined.
+//
+// With one tile per workgroup the loads of a tile are all in flight before
+// its compute, but nothing loads while it computes; at 3 resident workgroups
+// per CU that leaves HBM idle for a large part of each tile (the kernel with
+// its MFMA work removed runs in 60 % of the time).  Here each workgroup walks
+// tiles t, t + G, t + 2G, ... (G = 2 workgroups per CU) and issues the next
+// tile's global loads into registers before computing the current tile from
+// LDS, then stages them to LDS behind a barrier.  k is staged in LDS as well
+// (its fragments are plain 16-byte row reads), which keeps the prefetched set
+// to 28 16-byte loads per thread.  The arithmetic is the kernel above's.
+constexpr int kOPipeWGsPerCU = 2;
+
+template <int K, int V>
+struct OPCfg {
+  static constexpr int kPitch = V + 8;   // v, h rows (bf16 elements, 16-byte pad)
+  static constexpr int kKPitch = K + 8;  // k rows
+  static constexpr int kVTile = kBT * kPitch;
+  static constexpr int kHTile = K * kPitch;
+  static constexpr int kKTile = kBT * kKPitch;
+  static constexpr int kVLoads = kBT * (V / 8) / kOThreads;  // 16-byte loads per thread
+  static constexpr int kHLoads = K * (V / 4) / kOThreads;    // h is fp32
+  static constexpr int kKLoads = kBT * (K / 8) / kOThreads;
+  static constexpr int KS = K / 32;
+  static_assert(kBT * (V / 8) % kOThreads == 0 && K * (V / 4) % kOThreads == 0 &&
+                kBT * (K / 8) % kOThreads == 0, "staging split");
+};
+
+template <int K, int V>
+__global__ void __launch_bounds__(kOThreads, 2)
+chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                        const bf16* __restrict__ v, const float* __restrict__ g,
+                        const float* __restrict__ hs, bf16* __restrict__ o, float scale, int64_t T,
+                        int64_t H, int64_t NT, int64_t tiles) {
+  using C = OPCfg<K, V>;
+  constexpr int KS = C::KS;
+  constexpr int NB = V / 16;
+  __shared__ __attribute__((aligned(16))) bf16 lv[C::kVTile];
+  __shared__ __attribute__((aligned(16))) bf16 lh[C::kHTile];
+  __shared__ __attribute__((aligned(16))) bf16 lk[C::kKTile];
+  __shared__ float gs[kBT];
+
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
+  const int lane = tid & 63;
+  const int grp = lane >> 4;
+  const int li = lane & 15;
+  const int i = 16 * wv + li;  // this lane's query position
+
+  // Tile -> (b, c, head), head fastest (as the one-tile kernel).
+  auto tok_of = [&](int64_t tile, int64_t& hh) {
+    hh = tile % H;
+    const int64_t bc = tile / H;
+    const int64_t c = bc % NT, b = bc / NT;
+    return b * T + c * kBT;
+  };
+
+  // Prefetched registers of one tile.
+  u32x4 vr[C::kVLoads], hr[C::kHLoads], kr[C::kKLoads], qr[KS];
+  float gr = 0.f;
+  auto prefetch = [&](int64_t tile) {
+    int64_t hh;
+    const int64_t tok0 = tok_of(tile, hh);
+#pragma unroll
+    for (int it = 0; it < C::kHLoads; ++it) {
+      const int qi = tid + it * kOThreads;
+      const int r = qi / (V / 4), col = (qi - r * (V / 4)) * 4;
+      hr[it] = ldg16_nt(hs + tile * (int64_t)(K * V) + r * V + col);
+    }
+#pragma unroll
+    for (int it = 0; it < C::kVLoads; ++it) {
+      const int qi = tid + it * kOThreads;
+      const int j = qi / (V / 8), col = (qi - j * (V / 8)) * 8;
+      vr[it] = ldg16_nt(v + ((tok0 + j) * H + hh) * V + col);
+    }
+#pragma unroll
+    for (int it = 0; it < C::kKLoads; ++it) {
+      const int qi = tid + it * kOThreads;
+      const int j = qi / (K / 8), col = (qi - j * (K / 8)) * 8;
+      kr[it] = ldg16_nt(k + ((tok0 + j) * H + hh) * K + col);
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qr[s] = ldg16_nt(q + ((tok0 + i) * H + hh) * K + 32 * s + 8 * grp);
+    gr = (tid < kBT && g) ? g[(tok0 + tid) * H + hh] : 0.f;
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int it = 0; it < C::kVLoads; ++it) {
+      const int qi = tid + it * kOThreads;
+      const int j = qi / (V / 8), col = (qi - j * (V / 8)) * 8;
+      *reinterpret_cast<u32x4*>(lv + j * C::kPitch + col) = vr[it];
+    }
+#pragma unroll
+    for (int it = 0; it < C::kHLoads; ++it) {
+      const int qi = tid + it * kOThreads;
+      const int r = qi / (V / 4), col = (qi - r * (V / 4)) * 4;
+      float vals[4];
+      unpack16(hr[it], vals, 0.f);
+      lds_put4(lh + r * C::kPitch + col, nullptr, vals, false);
+    }
+#pragma unroll
+    for (int it = 0; it < C::kKLoads; ++it) {
+      const int qi = tid + it * kOThreads;
+      const int j = qi / (K / 8), col = (qi - j * (K / 8)) * 8;
+      *reinterpret_cast<u32x4*>(lk + j * C::kKPitch + col) = kr[it];
+    }
+    if (tid < kBT) gs[tid] = gr;
+  };
+
+  int64_t t = blockIdx.x;
+  if (t >= tiles) return;  // whole workgroup
+  prefetch(t);
+  stage();
+  lds_barrier();
+  for (;;) {
+    bf16x8 qh[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qh[s] = __builtin_bit_cast(bf16x8, qr[s]);
+    const int64_t tn = t + gridDim.x;
+    if (tn < tiles) prefetch(tn);  // in flight while tile t computes
+
+    int64_t hh;
+    const int64_t tok0 = tok_of(t, hh);
+    // Inter-chunk term, scaled by e^{g_i}.
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      acc[nb] = zero4();
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 hf = frag_tr(lh, C::kPitch, tr_row_natural(32 * s, 0), tr_row_natural(32 * s, 1), 16 * nb);
+        acc[nb] = mfma16x16x32(hf, qh[s], acc[nb]);
+      }
+    }
+    const float gi = gs[i];
+    const float egi = fast_exp(gi);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] *= egi;
+    // Gated, causally masked scores S^T[j][i] for key blocks jb <= wv.
+    f32x4 p[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      p[jb] = zero4();
+      if (jb > wv) continue;  // wave-uniform
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        p[jb] = mfma16x16x32(load8(lk + (16 * jb + li) * C::kKPitch + 32 * s + 8 * grp), qh[s], p[jb]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * jb + 4 * grp + r;
+        p[jb][r] = (j <= i) ? p[jb][r] * fast_exp(gi - gs[j]) : 0.f;
+      }
+    }
+    // Intra-chunk term, paired order.
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (2 * s > wv) continue;  // wave-uniform: both blocks fully masked
+      const float f[8] = {p[2 * s][0], p[2 * s][1], p[2 * s][2], p[2 * s][3],
+                          p[2 * s + 1][0], p[2 * s + 1][1], p[2 * s + 1][2], p[2 * s + 1][3]};
+      const bf16x8 ph = to_bf16x8(f);
+      const int r0 = tr_row_paired(32 * s, 0), r1 = tr_row_paired(32 * s, 1);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16x16x32(frag_tr(lv, C::kPitch, r0, r1, 16 * nb), ph, acc[nb]);
+    }
+    const int64_t orow = (tok0 + i) * H + hh;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) store4(o + orow * V + 16 * nb + 4 * grp, acc[nb] * scale);
+
+    if (tn >= tiles) break;
+    lds_barrier();  // every wave is done with tile t's LDS
+    stage();
+    lds_barrier();
+    t = tn;
+  }
+}
+
+template <int K, int V>
+hipError_t launch_o_pipe(const void* q, const void* k, const void* v, const void* g, const void* h,
+                         void* o, float scale, int64_t B, int64_t T, int64_t H, int64_t grid,
+                         hipStream_t s) {
+  const int64_t NT = T / kBT;
+  hipLaunchKernelGGL((chunk_fwd_o_pipe_kernel<K, V>), dim3((unsigned)grid), dim3(kOThreads), 0, s,
+                     (const bf16*)q, (const bf16*)k, (const bf16*)v, (const float*)g, (const float*)h,
+                     (bf16*)o, scale, T, H, NT, B * NT * H);
+  return hipGetLastError();
+}
+
 template <typename IT, int K, int V>
 hipError_t launch_o(const void* q, const void* k, const void* v, const void* g, const void* h,
                     void* o, float scale, int64_t B, int64_t T, int64_t H, hipStream_t s) {
@@ -251,6 +439,16 @@ template <typename IT>
 hipError_t dispatch_o(int64_t K, int64_t V, const void* q, const void* k, const void* v,
                       const void* g, const void* h, void* o, float scale, int64_t B, int64_t T,
                       int64_t H, hipStream_t s) {
+  if constexpr (std::is_same<IT, bf16>::value) {
+    const int64_t tiles = B * (T / kBT) * H;
+    const int64_t grid = (int64_t)device_cu_count() * kOPipeWGsPerCU;
+    if (grid > 0 && tiles >= 2 * grid) {
+      if (K == 64 && V == 64) return launch_o_pipe<64, 64>(q, k, v, g, h, o, scale, B, T, H, grid, s);
+      if (K == 64 && V == 128) return launch_o_pipe<64, 128>(q, k, v, g, h, o, scale, B, T, H, grid, s);
+      if (K == 128 && V == 64) return launch_o_pipe<128, 64>(q, k, v, g, h, o, scale, B, T, H, grid, s);
+      return launch_o_pipe<128, 128>(q, k, v, g, h, o, scale, B, T, H, grid, s);
+    }
+  }
   if (K == 64 && V == 64) return launch_o<IT, 64, 64>(q, k, v, g, h, o, scale, B, T, H, s);
   if (K == 64 && V == 128) return launch_o<IT, 64, 128>(q, k, v, g, h, o, scale, B, T, H, s);
   if (K == 128 && V == 64) return launch_o<IT, 128, 64>(q, k, v, g, h, o, scale, B, T, H, s);
