@@ -10,6 +10,7 @@
 //   probe_dpp_wave_shr1      : src[64] int32, old[64] int32 -> out[64] int32
 //   probe_cvt_bf16           : x[n] f32 -> y[n] bf16 (n even, n <= 4096)
 //   probe_quad_transpose     : x[64][4] f32 -> y[64][4] f32 (thm::quad_transpose)
+//   probe_mfma_16x16x4_f32   : a[64] f32, b[64] f32 -> c[64][4] f32
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -70,7 +71,18 @@ __global__ void __launch_bounds__(64) k_quad_transpose(const f32x4* x, f32x4* y)
   y[threadIdx.x] = thm::quad_transpose(x[threadIdx.x]);
 }
 
+__global__ void __launch_bounds__(64) k_mfma16f32(const float* a, const float* b, f32x4* c) {
+  const int l = threadIdx.x;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[l], b[l], acc, 0, 0, 0);
+  c[l] = acc;
+}
+
 extern "C" {
+int probe_mfma_16x16x4_f32(const void* a, const void* b, void* c, void* stream) {
+  hipLaunchKernelGGL(k_mfma16f32, dim3(1), dim3(64), 0, (hipStream_t)stream, (const float*)a, (const float*)b, (f32x4*)c);
+  return (int)hipGetLastError();
+}
 int probe_quad_transpose(const void* x, void* y, void* stream) {
   hipLaunchKernelGGL(k_quad_transpose, dim3(1), dim3(64), 0, (hipStream_t)stream, (const f32x4*)x, (f32x4*)y);
   return (int)hipGetLastError();

@@ -119,3 +119,21 @@ def test_quad_transpose(probe, dev):
         for i in range(4):
             exp[lane, i] = xc[(lane & ~3) + i, lane & 3]
     np.testing.assert_array_equal(yc, exp)
+
+
+def test_mfma_16x16x4_f32_layout(probe, dev):
+    # v_mfma_f32_16x16x4_f32: lane l holds A[m = l % 16][k = l // 16] and
+    # B[k = l // 16][n = l % 16]; the result D[m = 4 (l // 16) + r][n = l % 16]
+    # lands in c[l][r].  Integer-valued inputs make the products exact.
+    g = torch.Generator().manual_seed(5)
+    A = torch.randint(-8, 9, (16, 4), generator=g).float()
+    Bm = torch.randint(-8, 9, (4, 16), generator=g).float()
+    lanes = torch.arange(64)
+    a = A[lanes % 16, lanes // 16].contiguous().to(dev)
+    b = Bm[lanes // 16, lanes % 16].contiguous().to(dev)
+    c = torch.empty(64, 4, device=dev)
+    assert probe.probe_mfma_16x16x4_f32(P(a), P(b), P(c), S()) == 0
+    torch.cuda.synchronize()
+    D = A @ Bm
+    exp = torch.stack([D[4 * (lanes // 16) + r, lanes % 16] for r in range(4)], dim=1)
+    assert torch.equal(c.cpu(), exp)

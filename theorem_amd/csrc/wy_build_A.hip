@@ -5,22 +5,25 @@
 // `_build_A`, a torch matmul + solve_triangular); sign = +1 is the gated delta
 // rule's (I + M)^{-1}.  A [B, T, H, 64] fp32 holds row r of A_c at token c*64 + r.
 //
-// One wavefront per (b, chunk, head) tile, head fastest:
-//   1. k k^T on v_mfma_f32_16x16x32_bf16.  With lane (g, j) holding features
-//      8g .. 8g+7 of token j of a 16-token block, the A fragment of block ib
-//      and the B fragment of block jb are the same kind of 16-byte row load, so
-//      the tile's k is read from HBM exactly once, straight into registers
-//      (fp32 k: bf16 hi + lo, three products).  Only the 10 lower 16x16 tiles
-//      are formed.
-//   2. sign * M (strict lower part, scaled by beta_i e^{g_i - g_j}) goes to LDS
-//      as a packed triangle: row r holds its r entries, padded to a multiple of
-//      4 floats so it is read with 16-byte broadcast loads.
-//   3. Forward substitution in fp32: lane c holds column c of X = A_c and
-//      computes X[r][c] = delta_rc - sum_{s<r} (sign M)[r][s] X[s][c] for
-//      r = 0..63, fully unrolled (2016 FMAs per lane, two partial sums).
-//      The coefficient reads are LDS broadcasts whose latency the unrolled
-//      chain exposes: this step, not HBM, bounds the kernel.
-//   4. Row r of A_c is one 256-byte store (lane c writes column c).
+// One workgroup (4 wavefronts) per (b, chunk, head) tile, head fastest.  With
+// L = sign M (strictly lower) and 16x16 blocks L_ij, X = (I + L)^{-1} is block
+// lower triangular:
+//   X_ii = (I + L_ii)^{-1}                        (forward substitution)
+//   X_ij = -X_ii sum_{m=j}^{i-1} L_im X_mj        (i > j, by distance i - j)
+//   1. k k^T on v_mfma_f32_16x16x32_bf16: lane (g, j) holds features
+//      8g .. 8g+7 of token j of a 16-token block, so the A fragment of block ib
+//      and the B fragment of block jb are the same kind of 16-byte row load
+//      (fp32 k: bf16 hi + lo, three products).  The 10 lower blocks are spread
+//      over the 4 waves; every wave loads the tile's k (the repeats hit L2).
+//   2. L blocks (scaled by beta_i e^{g_i - g_j}, strict lower part) go to LDS.
+//   3. Wave w inverts the diagonal block w: lane c (< 16) owns column c and runs
+//      the 16-row substitution.
+//   4. The 6 off-diagonal blocks, 3 levels of independent blocks (3, 2, 1
+//      waves), each two fp32 MFMA products (v_mfma_f32_16x16x4_f32, exact fp32
+//      multiplies): T = sum L_im X_mj, then X_ij = -X_ii T, T passing through
+//      LDS to change from the accumulator to the operand layout.
+//   5. All 256 threads write A_c: 16-byte stores, 4 full 256-byte rows per
+//      wavefront instruction.
 // HBM traffic per tile: k, beta, g read once, A written once.
 #include <type_traits>
 
@@ -30,23 +33,42 @@ namespace thm {
 namespace {
 
 constexpr int kBT = 64;
+constexpr int kBP = 17;             // LDS pitch (floats) of a 16x16 block
+constexpr int kBlk = 16 * kBP;      // floats per block
+constexpr int kABThreads = 256;
 
-// Offset (floats) of packed row r: rows padded to multiples of 4.
-__host__ __device__ constexpr int tri_off(int r) {
-  int o = 0;
-  for (int q = 0; q < r; ++q) o += (q + 3) & ~3;
-  return o;
+// Packed index of lower block (i, j), j <= i < 4.
+__host__ __device__ constexpr int blk(int i, int j) { return i * (i + 1) / 2 + j; }
+
+__device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-constexpr int kTriFloats = tri_off(kBT);
+
+// acc += P Q for 16x16 blocks P, Q in LDS (pitch kBP): lane (g, l) feeds
+// P[l][4q + g] and Q[4q + g][l] at k-step q; acc[r] = row 4g + r, column l.
+__device__ __forceinline__ f32x4 block_mm(const float* P, const float* Q, f32x4 acc) {
+  const int lane = lane_id(), g = lane >> 4, l = lane & 15;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc = mfma16x16x4f32(P[l * kBP + 4 * q + g], Q[(4 * q + g) * kBP + l], acc);
+  return acc;
+}
+
+__device__ __forceinline__ void block_put(float* D, f32x4 acc, float sgn) {
+  const int lane = lane_id(), g = lane >> 4, l = lane & 15;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) D[(4 * g + r) * kBP + l] = sgn * acc[r];
+}
 
 template <typename IT, int K, int SIGN>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(kABThreads)
 wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
                   const float* __restrict__ g, float* __restrict__ A, int64_t T, int64_t H,
                   int64_t NT) {
   constexpr bool kSplit = std::is_same<IT, float>::value;
   constexpr int KS = K / 32;  // contraction steps
-  __shared__ __attribute__((aligned(16))) float lm[kTriFloats];
+  __shared__ float Lb[10 * kBlk];  // L = sign M, lower blocks (diagonal blocks: strict lower part)
+  __shared__ float Xb[10 * kBlk];  // X = A_c, lower blocks
+  __shared__ float Tb[3 * kBlk];   // per-level partial products
   __shared__ float sb[kBT], sg[kBT];
 
   const int64_t tile = blockIdx.x;
@@ -55,10 +77,12 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
   const int64_t c = bc % NT;
   const int64_t b = bc / NT;
   const int64_t tok0 = b * T + c * kBT;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
+  const int lane = tid & 63;
   const int grp = lane >> 4, li = lane & 15;
 
-  // k fragments: fr[tb][s] = k[tok0 + 16 tb + li][32 s + 8 grp .. + 7].
+  // 1. k fragments: fh[tb][s] = k[tok0 + 16 tb + li][32 s + 8 grp .. + 7].
   bf16x8 fh[4][KS], fl[4][kSplit ? KS : 1];
   {
     float v[8];
@@ -76,58 +100,95 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
       }
     }
   }
-  sb[lane] = beta[(tok0 + lane) * H + h];
-  sg[lane] = g ? g[(tok0 + lane) * H + h] : 0.f;
+  if (tid < kBT) {
+    sb[tid] = beta[(tok0 + tid) * H + h];
+    sg[tid] = g ? g[(tok0 + tid) * H + h] : 0.f;
+  }
   lds_barrier();
 
-  // sign * M into the packed triangle.
+  // 2. L blocks: wave w forms the lower blocks p = w, w + 4, w + 8 of the packed
+  //    order (compile-time block indices, so the fragments stay in registers).
 #pragma unroll
-  for (int ib = 0; ib < 4; ++ib) {
+  for (int p = 0; p < 10; ++p) {
+    if ((p & 3) != wv) continue;  // wave-uniform
+    constexpr int kIb[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
+    const int ib = kIb[p], jb = p - ib * (ib + 1) / 2;
+    f32x4 acc = zero4();
 #pragma unroll
-    for (int jb = 0; jb <= ib; ++jb) {
+    for (int s = 0; s < KS; ++s) {
+      acc = mfma16x16x32(fh[ib][s], fh[jb][s], acc);
+      if constexpr (kSplit) {
+        acc = mfma16x16x32(fh[ib][s], fl[jb][s], acc);
+        acc = mfma16x16x32(fl[ib][s], fh[jb][s], acc);
+      }
+    }
+    const int j = 16 * jb + li;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * ib + 4 * grp + r;
+      Lb[p * kBlk + (4 * grp + r) * kBP + li] =
+          (j < i) ? (float)SIGN * sb[i] * acc[r] * fast_exp(sg[i] - sg[j]) : 0.f;
+    }
+  }
+  lds_barrier();
+
+  // 3. Diagonal inverses: wave w, lane c < 16 owns column c of X_ww.
+  {
+    const float* L = Lb + blk(wv, wv) * kBlk;
+    float* X = Xb + blk(wv, wv) * kBlk;
+    if (lane < 16) {
+      float x[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float a0 = (r == lane) ? 1.f : 0.f, a1 = 0.f;
+#pragma unroll
+        for (int s = 0; s < r; ++s) {
+          if (s & 1) a1 = fmaf(-L[r * kBP + s], x[s], a1);
+          else a0 = fmaf(-L[r * kBP + s], x[s], a0);
+        }
+        x[r] = a0 + a1;
+        X[r * kBP + lane] = x[r];
+      }
+    }
+  }
+  lds_barrier();
+
+  // 4. Off-diagonal blocks by distance d = i - j: blocks (j + d, j), one wave each.
+#pragma unroll
+  for (int d = 1; d < 4; ++d) {
+    const int j = wv, i = wv + d;
+    const bool active = i < 4;  // wave-uniform
+    if (active) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        acc = mfma16x16x32(fh[ib][s], fh[jb][s], acc);
-        if constexpr (kSplit) {
-          acc = mfma16x16x32(fh[ib][s], fl[jb][s], acc);
-          acc = mfma16x16x32(fl[ib][s], fh[jb][s], acc);
-        }
+      for (int m = 0; m < 3; ++m) {
+        const int mm = j + m;
+        if (mm < i) acc = block_mm(Lb + blk(i, mm) * kBlk, Xb + blk(mm, j) * kBlk, acc);
       }
-      const int j = 16 * jb + li;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * ib + 4 * grp + r;
-        if (j < i) lm[tri_off(i) + j] = (float)SIGN * sb[i] * acc[r] * fast_exp(sg[i] - sg[j]);
-      }
+      block_put(Tb + wv * kBlk, acc, 1.f);
     }
-  }
-  lds_barrier();
-
-  // Forward substitution, lane = column; coefficients are 16-byte LDS
-  // broadcasts, two partial sums per row.
-  float X[kBT];
-#pragma unroll
-  for (int r = 0; r < kBT; ++r) {
-    float a0 = (r == lane) ? 1.f : 0.f, a1 = 0.f;
-#pragma unroll
-    for (int s4 = 0; s4 < (r + 3) / 4; ++s4) {
-      const f32x4 l4 = *reinterpret_cast<const f32x4*>(lm + tri_off(r) + 4 * s4);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int s = 4 * s4 + q;
-        if (s < r) {
-          if (q & 1) a1 = fmaf(-l4[q], X[s], a1);
-          else a0 = fmaf(-l4[q], X[s], a0);
-        }
-      }
+    lds_barrier();
+    if (active) {
+      const f32x4 acc = block_mm(Xb + blk(i, i) * kBlk, Tb + wv * kBlk, zero4());
+      block_put(Xb + blk(i, j) * kBlk, acc, -1.f);
     }
-    X[r] = a0 + a1;
+    lds_barrier();
   }
 
-  float* out = A + (tok0 * H + h) * kBT + lane;
+  // 5. A_c rows: thread (r = q / 16, chunk j4 = q % 16) writes A[r][4 j4 .. + 3].
+  float* out = A + (tok0 * H + h) * kBT;
 #pragma unroll
-  for (int r = 0; r < kBT; ++r) out[r * H * kBT] = X[r];
+  for (int it = 0; it < kBT * 16 / kABThreads; ++it) {
+    const int q = tid + it * kABThreads;
+    const int r = q >> 4, j0 = (q & 15) * 4;
+    const int ib = r >> 4, jb = j0 >> 4;
+    f32x4 v = zero4();
+    if (jb <= ib) {
+      const float* X = Xb + blk(ib, jb) * kBlk + (r & 15) * kBP + (j0 & 15);
+      v[0] = X[0]; v[1] = X[1]; v[2] = X[2]; v[3] = X[3];
+    }
+    *reinterpret_cast<f32x4*>(out + (int64_t)r * H * kBT + j0) = v;
+  }
 }
 
 template <typename IT, int K>
@@ -136,10 +197,10 @@ hipError_t launch_A(const void* k, const void* beta, const void* g, void* A, int
   const int64_t NT = T / kBT;
   const dim3 grid((unsigned)(B * NT * H));
   if (sign < 0)
-    hipLaunchKernelGGL((wy_build_A_kernel<IT, K, -1>), grid, dim3(64), 0, s, (const IT*)k,
+    hipLaunchKernelGGL((wy_build_A_kernel<IT, K, -1>), grid, dim3(kABThreads), 0, s, (const IT*)k,
                        (const float*)beta, (const float*)g, (float*)A, T, H, NT);
   else
-    hipLaunchKernelGGL((wy_build_A_kernel<IT, K, 1>), grid, dim3(64), 0, s, (const IT*)k,
+    hipLaunchKernelGGL((wy_build_A_kernel<IT, K, 1>), grid, dim3(kABThreads), 0, s, (const IT*)k,
                        (const float*)beta, (const float*)g, (float*)A, T, H, NT);
   return hipGetLastError();
 }
@@ -158,8 +219,8 @@ extern "C" int thm_wy_build_A(const void* k, const void* beta, const void* g, vo
   if (K != 64 && K != 128) return THM_ERR_UNSUPPORTED;
   if (B == 0 || T == 0) return THM_OK;  // empty: nothing is read or written
   if (!k || !beta || !A) return THM_ERR_NULL_POINTER;
-  if ((uintptr_t)k % 16) return THM_ERR_MISALIGNED;
-  if (((uintptr_t)beta % 4) || ((uintptr_t)A % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
+  if (((uintptr_t)k % 16) || ((uintptr_t)A % 16)) return THM_ERR_MISALIGNED;
+  if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
