@@ -14,7 +14,9 @@ is read from profiles/traffic_cfg4.json when that summary of rocprofv3
 FETCH_SIZE / WRITE_SIZE runs exists, else null.  ``cpu_baseline`` times the
 CPU oracle on a bounded sample (one batch element of the same workload) and
 scales to a full step.  ``shapes`` gives each kernel's latency at configs 0-3,
-the shapes the reference publishes numbers for.
+the shapes the reference publishes numbers for; ``extensions`` times the
+kernels beyond the four (WY matrix, gate cumsum, channels-last conv, conv
+decode step) at config-4 sizes.
 """
 from __future__ import annotations
 
@@ -190,6 +192,53 @@ def shape_latencies(torch, dev, warmup: int = 5, iters: int = 50, batched: int =
     return out
 
 
+# --------------------------------------------------------------------------- extensions
+
+def work_build_A(B, T, H, K, eb=2):
+    N = B * T * H
+    return N * K * eb + N * 8 + N * 64 * 4
+
+
+def extension_timings(torch, inp, conv_in, iters: int = 10):
+    """The kernels beyond the four (WY matrix, gate cumsum, channels-last conv,
+    conv decode step) at config-4 sizes: HIP events around ``iters``
+    back-to-back launches after one warm-up."""
+    from theorem_amd import chain
+    from theorem_amd.kernels import causal_conv1d, recompute_w_u
+
+    B, T, H, K = inp["k"].shape
+    x, w, b = conv_in
+    Bc, D, S = x.shape
+    xcl = x.transpose(1, 2).contiguous().transpose(1, 2)
+    a = torch.randn(B, T, H, device=x.device)
+    state = torch.zeros(Bc, D, w.shape[1] - 1, dtype=x.dtype, device=x.device)
+    xt = x[:, :, 0].contiguous()
+    cases = {
+        "wy_build_A": (lambda: recompute_w_u.build_A(inp["k"], inp["beta"], inp["g"], sign=+1),
+                       work_build_A(B, T, H, K), f"({B},{T},{H},K={K}) bf16 k, sign +1"),
+        "chunk_local_cumsum": (lambda: chain.chunk_local_cumsum(a, logsigmoid=True), B * T * H * 8,
+                               f"({B},{T},{H}) fp32, logsigmoid"),
+        "causal_conv1d_channels_last": (lambda: causal_conv1d.custom_kernel((xcl, w, b)),
+                                        work_conv(Bc, D, S, w.shape[1])[0], f"({Bc},{S},{D}) bf16 [B,S,D]"),
+        "causal_conv1d_update": (lambda: causal_conv1d.causal_conv1d_update(xt, state, w, b),
+                                 Bc * D * (2 * 2 + 2 * (w.shape[1] - 1) * 2), f"({Bc},{D}) bf16, one token"),
+    }
+    out = {}
+    for name, (fn, by, shape) in cases.items():
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        out[name] = {"us": round(us, 2), "shape": shape, "bytes": by, "GBps": round(by / us / 1e3, 1),
+                     "hbm_frac": round(by / (us * 1e-6) / HBM_PEAK, 4)}
+    return out
+
+
 # --------------------------------------------------------------------------- main
 
 def main() -> int:
@@ -199,8 +248,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape latencies of configs 0-3")
+    ap.add_argument("--no-ext", action="store_true", help="skip the extension kernels (A-builder, gate cumsum, ...)")
     ap.add_argument("--small", action="store_true", help="1/8-size workload (quick check)")
-    ap.add_argument("--only", choices=["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o"],
+    ap.add_argument("--only", choices=["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o", "wy_build_A"],
                     help="run only this kernel of the step (for per-kernel rocprofv3 counter runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (rocprofv3 counter calibration)")
@@ -269,6 +319,7 @@ def main() -> int:
                 recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V)),
             "chunk_fwd_h": lambda: chunk_fwd_h.custom_kernel(dict(k=k, w=w, u=u, g=g, output_final_state=True)),
             "chunk_fwd_o": lambda: chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=vn, g=g, h=h, scale=scale)),
+            "wy_build_A": lambda: recompute_w_u.build_A(k, beta, g, sign=+1),
         }[args.only]
         for _ in range(args.warmup + args.steps):
             run()
@@ -321,6 +372,11 @@ def main() -> int:
         print("[bench] per-shape latencies (configs 0-3)", file=sys.stderr, flush=True)
         shapes = shape_latencies(torch, dev)
 
+    ext = None
+    if not args.no_ext and not args.small:
+        print("[bench] extension kernels", file=sys.stderr, flush=True)
+        ext = extension_timings(torch, inp, conv_in)
+
     cpu = None
     if not args.no_cpu:
         print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
@@ -334,7 +390,7 @@ def main() -> int:
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded torch CPU generator; BASELINE.json config-4 distributions)",
         "config": {"workload": workload, "parallelism": "single GPU"},
-        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu, "shapes": shapes,
+        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu, "shapes": shapes, "extensions": ext,
     }
     print(json.dumps(line))
     return 0
