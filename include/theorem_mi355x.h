@@ -163,6 +163,25 @@ int thm_chunk_fwd_o(const void* q, const void* k, const void* v, const void* g,
                     int32_t chunk_size, int32_t qkv_dtype, void* stream);
 
 /*
+ * Fused chunked Gated DeltaNet forward (delta form): per (b, head) and chunk c,
+ *   v_new = u_c - w_c S;
+ *   o_c = scale * ( exp(g_i) q_i . S + sum_{j<=i} (q_i . k_j) exp(g_i - g_j) v_new_j );
+ *   S <- exp(g_last) S + (k_c * exp(g_last - g_c))^T v_new
+ * i.e. thm_chunk_fwd_h (flags = THM_H_DELTA) followed by thm_chunk_fwd_o with
+ * h[c] = the state before chunk c, without writing the per-chunk states.
+ * Replaces the composition of kernels/chunk_fwd_h/kernel.py:141-191 and
+ * kernels/chunk_fwd_o/kernel.py:146-212 in the chunked forward; no single
+ * reference function does this.
+ *   bf16 only (qkv_dtype = THM_DTYPE_BF16): q, k, w, u, o, v_new bf16;
+ *   g, h0, ht fp32.  g, h0, v_new, ht may be NULL.  K, V in {64, 128};
+ *   T % 64 == 0.
+ */
+int thm_chunk_gated_delta_fwd(const void* q, const void* k, const void* w, const void* u,
+                              const void* g, const void* h0, void* o, void* v_new, void* ht,
+                              float scale, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                              int32_t chunk_size, int32_t qkv_dtype, void* stream);
+
+/*
  * WY matrix of the chunked Gated DeltaNet forward, per chunk c of
  * chunk_size = 64 tokens:
  *   M[i][j] = beta_i (k_i . k_j) exp(g_i - g_j) for j < i (0 on and above the diagonal),

@@ -115,6 +115,17 @@ def test_cfg4_build_A_full(chain):
     assert dev <= 1e-4 * float(d["A"].abs().max()), f"A max |diff| {dev:.3e}"
 
 
+def test_cfg4_fused_forward(chain):
+    # The fused h + o kernel at full size against the two separate kernels.
+    from theorem_amd.chain import chunk_fwd_fused
+    d = chain
+    o, _, ht = chunk_fwd_fused(d["q"], d["k"], d["w"], d["u"], d["g"], d["scale"], None, True)
+    torch.cuda.synchronize()
+    for what, got, ref in (("o", o, d["o"]), ("final state", ht, d["ht"])):
+        dev_ = float((got.float() - ref.float()).abs().max())
+        assert dev_ <= 1e-2 * (1 + float(ref.float().abs().max())), f"fused {what}: max |diff| {dev_:.3e}"
+
+
 def test_cfg4_homogeneity(chain):
     # w, u are linear in A; h, v_new, final state are linear in u (zero initial
     # state); o is linear in (v, h) jointly.

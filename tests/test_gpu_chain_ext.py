@@ -115,3 +115,41 @@ def test_chain_from_per_token_gates(dev, K, V):
     eo, eS = odn.gated_delta_rule_tokens(np_(q), np_(k), np_(v), np_(beta), a, scale)
     assert_close(o, eo, 1e-2, 1e-2, "chain o")
     assert_close(ht, eS, 1e-2, 1e-2, "chain final state")
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (64, 128), (128, 64), (128, 128)])
+@pytest.mark.parametrize("gate", ["logsigmoid", None])
+def test_fused_forward_matches_two_kernels_and_oracle(dev, K, V, gate):
+    # chunk_fwd_fused = chunk_fwd_h (delta form) followed by chunk_fwd_o, without
+    # the per-chunk states: against the two kernels and the float64 oracle.
+    from theorem_amd.kernels import chunk_fwd_h, chunk_fwd_o
+    B, T, H = 2, 320, 3
+    d = configs.make_h_inputs(B, T, H, K, V, seed=31, device=dev, dtype=torch.bfloat16,
+                              gate=gate or "zero", h0_std=0.1)
+    gen = torch.Generator().manual_seed(32)
+    q = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16).to(dev)
+    g = d["g"] if gate else None
+    scale = K ** -0.5
+    o, vn, ht = chain.chunk_fwd_fused(q, d["k"], d["w"], d["u"], g, scale, d["h0"], True, True)
+    h, vn2, ht2 = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=g, initial_state=d["h0"],
+                                                 output_final_state=True))
+    o2 = chunk_fwd_o.custom_kernel(dict(q=q, k=d["k"], v=vn2, g=g, h=h, scale=scale))
+    torch.cuda.synchronize()
+    assert o.dtype == torch.bfloat16 and o.shape == (B, T, H, V)
+    assert_close(o, o2, 1e-2, 1e-2, f"fused o vs two kernels K={K} V={V} gate={gate}")
+    assert_close(vn, vn2, 1e-2, 1e-2, "v_new")
+    assert_close(ht, ht2, 1e-2, 1e-2, "final state")
+    gk = np_(g) if g is not None else None
+    eh, evn, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np_(d["w"]), np_(d["u"]), gk, h0=np_(d["h0"]))
+    eo = odn.chunk_fwd_o_diff(np_(q), np_(d["k"]), evn, gk, eh, scale)
+    assert_close(o, eo, 1e-2, 1e-2, f"fused o vs oracle K={K} V={V} gate={gate}")
+    assert_close(ht, eht, 1e-2, 1e-2, "final state vs oracle")
+    # Optional outputs may be omitted; T = 0 returns the initial state.
+    o3, vn3, ht3 = chain.chunk_fwd_fused(q, d["k"], d["w"], d["u"], g, scale, d["h0"])
+    torch.cuda.synchronize()
+    assert vn3 is None and ht3 is None and torch.equal(o3, o)
+    e0 = torch.empty(B, 0, H, K, device=dev, dtype=torch.bfloat16)
+    _, _, ht0 = chain.chunk_fwd_fused(e0, e0, e0, torch.empty(B, 0, H, V, device=dev, dtype=torch.bfloat16),
+                                      None, scale, d["h0"], True)
+    torch.cuda.synchronize()
+    assert torch.equal(ht0, d["h0"])

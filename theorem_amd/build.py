@@ -28,6 +28,7 @@ SOURCES = [
     "recompute_w_u.hip",
     "chunk_fwd_h.hip",
     "chunk_fwd_o.hip",
+    "chunk_fwd_fused.hip",
     "wy_build_A.hip",
     "gates.hip",
 ]

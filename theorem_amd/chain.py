@@ -4,6 +4,7 @@
     (w, u) = recompute_w_u(k, v, beta, A, g)                            HIP
     (h, v_new, S) = chunk_fwd_h delta form (h[c] before chunk c)        HIP
     o      = chunk_fwd_o(q, k, v_new, g, h, scale)                      HIP
+    (the last two fused into one kernel for bf16: chunk_fwd_fused)
 
 The reference never composes its ops (each is tested alone); this is the
 forward of chunked Gated DeltaNet that the three ops are the stages of, and
@@ -42,12 +43,41 @@ def build_A(k: torch.Tensor, beta: torch.Tensor, g: torch.Tensor | None) -> torc
     return recompute_w_u.build_A(k, beta, g, sign=+1)
 
 
+def chunk_fwd_fused(q, k, w, u, g, scale: float, initial_state=None, output_final_state: bool = False,
+                    save_new_value: bool = False):
+    """o (and optionally v_new, final state) of chunk_fwd_h (delta form) followed
+    by chunk_fwd_o, in one HIP kernel that never writes the per-chunk states
+    (thm_chunk_gated_delta_fwd; bf16 q, k, w, u).  Returns (o, v_new or None, ht or None)."""
+    B, T, H, K = k.shape
+    V = u.shape[-1]
+    assert T % BT == 0, f"T={T} must be a multiple of {BT}"
+    assert q.shape == k.shape == w.shape and u.shape[:3] == (B, T, H)
+    assert q.dtype == k.dtype == w.dtype == u.dtype == torch.bfloat16, "the fused path is bf16-only"
+    _capi.require_device(q, k, w, u, g, initial_state)
+    for name, t in (("g", g), ("initial_state", initial_state)):
+        _capi.require_f32(t, name)
+    q, k, w, u, g, h0 = (_capi.prep(t, n) for t, n in ((q, "q"), (k, "k"), (w, "w"), (u, "u"), (g, "g"),
+                                                       (initial_state, "initial_state")))
+    o = torch.empty_like(u)
+    vn = torch.empty_like(u) if save_new_value else None
+    ht = torch.empty(B, H, K, V, dtype=torch.float32, device=k.device) if output_final_state else None
+    status = _capi.load_library().thm_chunk_gated_delta_fwd(
+        _capi.ptr(q), _capi.ptr(k), _capi.ptr(w), _capi.ptr(u), _capi.ptr(g), _capi.ptr(h0), _capi.ptr(o),
+        _capi.ptr(vn), _capi.ptr(ht), float(scale), B, T, H, K, V, BT, _capi.THM_DTYPE[torch.bfloat16],
+        _capi.stream_of(k))
+    _capi.check(status, "thm_chunk_gated_delta_fwd")
+    return o, vn, ht
+
+
 def chunk_gated_delta_rule_fwd(q, k, v, beta, g, scale: float, initial_state=None,
                                output_final_state: bool = False, A: torch.Tensor | None = None,
                                return_intermediates: bool = False, a: torch.Tensor | None = None,
-                               a_logsigmoid: bool = False):
+                               a_logsigmoid: bool = False, fused: bool | None = None):
     """o [B, T, H, V] (dtype of q) and the final state [B, H, K, V] fp32 (or None).
 
+    bf16 inputs run the state recurrence and the output in one fused kernel
+    (``fused``, default for bf16 unless ``return_intermediates``, which needs
+    the per-chunk states h); otherwise chunk_fwd_h then chunk_fwd_o.
     ``g`` is the chunk-local cumulative log decay [B, T, H] fp32 (or None: no
     gate).  Alternatively pass the per-token log decay ``a`` (g = None): g is
     then formed on the GPU by chunk_local_cumsum(a), of log(sigmoid(a)) when
@@ -60,6 +90,11 @@ def chunk_gated_delta_rule_fwd(q, k, v, beta, g, scale: float, initial_state=Non
     if A is None:
         A = build_A(k, beta, g)
     w, u = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V))
+    if fused is None:
+        fused = k.dtype == torch.bfloat16 and not return_intermediates
+    if fused:
+        o, _, ht = chunk_fwd_fused(q, k, w, u, g, scale, initial_state, output_final_state)
+        return o, ht
     h, v_new, ht = chunk_fwd_h.custom_kernel(dict(k=k, w=w, u=u, g=g, initial_state=initial_state,
                                                   output_final_state=output_final_state))
     o = chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=v_new, g=g, h=h, scale=scale))
