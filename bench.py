@@ -201,8 +201,8 @@ def work_build_A(B, T, H, K, eb=2):
 
 def extension_timings(torch, inp, conv_in, iters: int = 10):
     """The kernels beyond the four (WY matrix, gate cumsum, channels-last conv,
-    conv decode step) at config-4 sizes: HIP events around ``iters``
-    back-to-back launches after one warm-up."""
+    conv decode step, fused h + o, the whole chunked forward) at config-4
+    sizes: HIP events around ``iters`` back-to-back launches after one warm-up."""
     from theorem_amd import chain
     from theorem_amd.kernels import causal_conv1d, recompute_w_u
 
@@ -223,6 +223,19 @@ def extension_timings(torch, inp, conv_in, iters: int = 10):
         "causal_conv1d_update": (lambda: causal_conv1d.causal_conv1d_update(xt, state, w, b),
                                  Bc * D * (2 * 2 + 2 * (w.shape[1] - 1) * 2), f"({Bc},{D}) bf16, one token"),
     }
+    V = inp["v"].shape[-1]
+    ww, uu = recompute_w_u.custom_kernel(recompute_w_u.Data(
+        k=inp["k"], v=inp["v"], beta=inp["beta"], A=inp["A"], g=inp["g"], B=B, T=T, H=H, K=K, V=V))
+    N = B * T * H
+    cases["chunk_gated_delta_fwd"] = (
+        lambda: chain.chunk_fwd_fused(inp["q"], inp["k"], ww, uu, inp["g"], inp["scale"], None, True),
+        N * (3 * K * 2 + V * 2 + 4) + N * V * 2 + B * H * K * V * 4,
+        f"({B},{T},{H},{K},{V}) bf16: chunk_fwd_h + chunk_fwd_o fused, final state out")
+    cases["chunk_gated_delta_rule_fwd"] = (
+        lambda: chain.chunk_gated_delta_rule_fwd(inp["q"], inp["k"], inp["v"], inp["beta"], inp["g"], inp["scale"],
+                                                 output_final_state=True),
+        work_build_A(B, T, H, K) + work_wu(B, T, H, K, V)[0] + N * (3 * K * 2 + V * 2 + 4) + N * V * 2,
+        "the whole chunked forward from (q, k, v, beta, g): A-builder, recompute_w_u, fused h + o")
     out = {}
     for name, (fn, by, shape) in cases.items():
         fn()
@@ -250,7 +263,8 @@ def main() -> int:
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape latencies of configs 0-3")
     ap.add_argument("--no-ext", action="store_true", help="skip the extension kernels (A-builder, gate cumsum, ...)")
     ap.add_argument("--small", action="store_true", help="1/8-size workload (quick check)")
-    ap.add_argument("--only", choices=["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o", "wy_build_A"],
+    ap.add_argument("--only", choices=["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o", "wy_build_A",
+                                        "chunk_gated_delta_fwd"],
                     help="run only this kernel of the step (for per-kernel rocprofv3 counter runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (rocprofv3 counter calibration)")
@@ -274,7 +288,7 @@ def main() -> int:
         print(json.dumps({"copy_calib_bytes": src.numel() * 4, "launches": args.warmup + args.steps}))
         return 0
 
-    from theorem_amd import configs
+    from theorem_amd import chain, configs
     from theorem_amd.kernels import causal_conv1d, chunk_fwd_h, chunk_fwd_o, recompute_w_u
 
     dev = torch.device("cuda:0")
@@ -320,6 +334,7 @@ def main() -> int:
             "chunk_fwd_h": lambda: chunk_fwd_h.custom_kernel(dict(k=k, w=w, u=u, g=g, output_final_state=True)),
             "chunk_fwd_o": lambda: chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=vn, g=g, h=h, scale=scale)),
             "wy_build_A": lambda: recompute_w_u.build_A(k, beta, g, sign=+1),
+            "chunk_gated_delta_fwd": lambda: chain.chunk_fwd_fused(q, k, w, u, g, scale, None, True),
         }[args.only]
         for _ in range(args.warmup + args.steps):
             run()

@@ -30,8 +30,10 @@
 // All DMA and stores of the chunk loop go through vmem.h, and the wait at the
 // top of the loop is an exact count (one chunk of stores is issued after each
 // chunk's DMA).
-// HBM traffic per token-head: k, w, q (2K bf16 bytes each... 3 K eb), u (V eb),
-// g (4 B) read once; o (V eb) written once (+ v_new when requested).
+// HBM traffic per token-head: k, w and q (K eb each), u (V eb) and g (4 B)
+// read once; o (V eb) written once (+ v_new when requested).  The V-tiles of
+// one (b, head) run on one XCD, so their second read of k, w, q is meant to
+// hit that XCD's L2.
 #include "h_layout.h"
 #include "mfma.h"
 #include "vmem.h"
