@@ -12,24 +12,29 @@
 // state before chunk c; nothing of either reference kernel's output but o
 // (and optionally v_new and the final state) is written.
 //
-// Structure (the bf16 DMA pipeline of chunk_fwd_h.hip, 4 wavefronts, wave wq
-// owns state columns 16 wq .. 16 wq + 15 of the tile for all K rows):
+// Structure: one 512-thread workgroup per (b, head, V-tile), 8 wavefronts in
+// two roles that share SIMDs pairwise; wave role and column group wq (columns
+// 16 wq .. 16 wq + 15 of the tile) are wave-uniform:
 //   * k, w, q, u and g of a chunk arrive by global -> LDS DMA into a 2-stage
-//     ring (XOR-swizzled tiles of h_layout.h), one chunk ahead of use;
-//   * P1: v_new = u - w S, the S accumulator pairs as the B operand (paired
-//     contraction order), w rows from LDS in the same order;
-//   * per 16-row query block ib:
-//       global term  q S     -- the same product as P1 with q rows;
-//       scores P^T[j][i] = k_j . q_i (natural order), gated and masked
-//       (diagonal included); their accumulator pairs are directly the A
-//       operand of the local term P v_new, whose B operand is the v_new
-//       accumulator pairs; each wave forms the scores it needs itself;
-//       o = scale (e^{g_i} q S + P v_new), an 8-byte store per lane after a
-//       4x4 quad transpose;
-//   * P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
-// All DMA and stores of the chunk loop go through vmem.h, and the wait at the
-// top of the loop is an exact count (one chunk of stores is issued after each
-// chunk's DMA).
+//     ring (XOR-swizzled tiles of h_layout.h), one chunk ahead of use, issued
+//     by the state waves;
+//   * state waves (0-3) hold S[K x 16 columns] in fp32 registers.  Phase 1:
+//     hand S to the output waves as bf16 B-operand pairs (LDS), P1 v_new =
+//     u - w S (the S pairs as the B operand, paired contraction order), hand
+//     v_new over the same way.  Phase 2: P2 S = e^{g_last} S +
+//     k^T (v_new e^{g_last - g});
+//   * output waves (4-7).  Phase 1: the scores P[i][j] = (q_i . k_j)
+//     e^{g_i - g_j}, j <= i (diagonal included), each wave 2 or 3 of the ten
+//     16 x 16 lower-triangle blocks, written to LDS as bf16.  Phase 2, per
+//     16-row query block: global term q S from the handed-over S pairs,
+//     local term P v_new (P rows as the A operand, the v_new pairs as B),
+//     o = scale (e^{g_i} q S + P v_new) as one 8-byte store per lane after a
+//     4x4 quad transpose;
+//   * a barrier at the top of each chunk (its tiles are in LDS, chunk c - 1
+//     is finished) and one between the phases.
+// All DMA and stores of the chunk loop go through vmem.h, and the state waves'
+// wait at the top of the loop is an exact count (their v_new stores of one
+// chunk are issued after each chunk's DMA); the output waves issue stores only.
 // HBM traffic per token-head: k, w and q (K eb each), u (V eb) and g (4 B)
 // read once; o (V eb) written once (+ v_new when requested).  The V-tiles of
 // one (b, head) run on one XCD, so their second read of k, w, q is meant to
@@ -43,7 +48,7 @@ namespace {
 
 constexpr int kBT = 64;
 constexpr int kFBV = 64;        // V-tile width
-constexpr int kFThreads = 256;  // 4 wavefronts x 16 state columns
+constexpr int kFThreads = 512;  // 4 state + 4 output wavefronts
 constexpr int kFStages = 2;
 
 template <int K, bool HAS_G, bool STORE_VN>
@@ -52,14 +57,17 @@ struct FCfg {
   static constexpr int kTileK = kBT * kRowK;
   static constexpr int kRowU = kFBV * 2;          // bytes per u row of the V-tile
   static constexpr int kTileU = kBT * kRowU;
-  static constexpr int kGBytes = 4 * kBT * 4;     // one gate copy per wave
+  static constexpr int kGBytes = 4 * kBT * 4;     // one gate copy per state wave
   static constexpr int kStage = 3 * kTileK + kTileU + (HAS_G ? kGBytes : 0);
-  static constexpr int kLds = kFStages * kStage;
-  static constexpr int KB = K / 16;               // 16-row state tiles per wave
-  static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per wave per k / w / q tile
+  static constexpr int KB = K / 16;               // 16-row state tiles per column group
+  static constexpr int kPBytes = kBT * kBT * 2;   // the chunk's scores P, bf16
+  static constexpr int kSBytes = 4 * (KB / 2) * 64 * 16;  // S handed over as bf16 B-operand pairs
+  static constexpr int kVBytes = 4 * 2 * 64 * 16;         // v_new handed over the same way
+  static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes;
+  static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per state wave per k / w / q tile
   static constexpr int kUDma = kTileU / 1024 / 4;
   static constexpr int kDma = 3 * kKDma + kUDma + (HAS_G ? 1 : 0);
-  static constexpr int kStores = 4 + (STORE_VN ? 4 : 0);  // o (+ v_new) row tiles per wave
+  static constexpr int kStores = STORE_VN ? 4 : 0;  // v_new row tiles per state wave
   static constexpr int kWaitFirst = (kFStages - 2) * kDma;
   static constexpr int kWaitSteady = (kFStages - 1) * kStores + (kFStages - 2) * kDma;
   static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
@@ -76,6 +84,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                        float scale, int64_t T, int64_t H, int64_t NT, int64_t BH) {
   using C = FCfg<K, HAS_G, STORE_VN>;
   constexpr int NVT = V / kFBV;
+  constexpr int KB2 = C::KB / 2;
   __shared__ __attribute__((aligned(1024))) char lds[C::kLds];
 
   const int64_t blk = blockIdx.x;
@@ -92,7 +101,9 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   const int v0 = (int)vt * kFBV;
 
   const int tid = threadIdx.x;
-  const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wi = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool state_wave = wi < 4;  // waves 0-3: recurrence; waves 4-7: output
+  const int wq = wi & 3;           // column group 16 wq .. 16 wq + 15 of the tile
   const int lane = tid & 63, grp = lane >> 4, li = lane & 15;
 
   auto stage_k = [&](int s) { return lds + s * C::kStage; };
@@ -102,6 +113,10 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   auto stage_g = [&](int s) {
     return reinterpret_cast<float*>(lds + s * C::kStage + 3 * C::kTileK + C::kTileU);
   };
+  char* const lp = lds + kFStages * C::kStage;  // P[i][j], 128-byte rows, swizzled
+  // Hand-over slots, lane-major: 16 bytes per lane per B-operand pair.
+  bf16x8* const ls = reinterpret_cast<bf16x8*>(lp + C::kPBytes) + wq * KB2 * 64 + lane;
+  bf16x8* const lv = reinterpret_cast<bf16x8*>(lp + C::kPBytes + C::kSBytes) + wq * 2 * 64 + lane;
 
   // Global geometry in bytes.  Token t of chunk c, head hh: ((b T + 64 c + t) H + hh) D.
   const int64_t tsk = H * K * 2, tsv = H * V * 2;
@@ -123,6 +138,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   }
   const uint32_t goff = (uint32_t)(lane * H * 4);
 
+  // DMA of chunk cc into stage s; issued by the state waves only.
   auto issue = [&](int64_t cc, int s) {
     const int64_t off = kc0 + cc * kcs;
     const char* srcs[3] = {reinterpret_cast<const char*>(k) + off, reinterpret_cast<const char*>(w) + off,
@@ -144,16 +160,20 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     }
   };
 
-  // State S[kappa = 16 kb + 4 grp + r][n = v0 + 16 wq + li] in S[kb][r].
-  f32x4 S[C::KB];
-  const int ncol = v0 + 16 * wq + li;
-  const int64_t st_base = bh * (int64_t)(K * V);
+  // rows x S for a 16-row block of a [64 x K] tile (w or q): A = tile rows,
+  // B = the S pairs sbv, paired contraction order.
+  auto rows_times_S = [&](const char* tile, int ib, const bf16x8* sbv) {
+    f32x4 acc = zero4();
+    const int row = 16 * ib + li;
 #pragma unroll
-  for (int kb = 0; kb < C::KB; ++kb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      S[kb][r] = h0 ? h0[st_base + (int64_t)(16 * kb + 4 * grp + r) * V + ncol] : 0.f;
-  wait_vmcnt<0>();  // retire the h0 loads before the counted loop
+    for (int s2 = 0; s2 < KB2; ++s2) {
+      const int e0 = 32 * s2 + 4 * grp;
+      const bf16x4 a0 = *reinterpret_cast<const bf16x4*>(tile + hl::tile_off(row, e0, C::kRowK));
+      const bf16x4 a1 = *reinterpret_cast<const bf16x4*>(tile + hl::tile_off(row, e0 + 16, C::kRowK));
+      acc = mfma16x16x32(concat(a0, a1), sbv[s2], acc);
+    }
+    return acc;
+  };
 
   // Row-tile stores after the quad transpose: lane (grp, 4 m4 + qq) holds row
   // 4 grp + qq of a 16-row tile at columns 16 wq + 4 m4 .. + 3.
@@ -166,148 +186,171 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     st_b64(base, rowoff0 + (uint32_t)(16 * ib * tsv), __builtin_bit_cast(u32x2, ov));
   };
 
-  if (NT > 0) issue(0, 0);
+  // State S[kappa = 16 kb + 4 grp + r][n = v0 + 16 wq + li] in S[kb][r] (state waves).
+  f32x4 S[C::KB];
+  const int ncol = v0 + 16 * wq + li;
+  const int64_t st_base = bh * (int64_t)(K * V);
+#pragma unroll
+  for (int kb = 0; kb < C::KB; ++kb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[kb][r] = (state_wave && h0) ? h0[st_base + (int64_t)(16 * kb + 4 * grp + r) * V + ncol] : 0.f;
+  wait_vmcnt<0>();  // retire the h0 loads before the counted loop
+
+  if (state_wave && NT > 0) issue(0, 0);
   for (int64_t c = 0; c < NT; ++c) {
     const int s = (int)(c % kFStages);
-    if (c < kFStages - 1) wait_vmcnt<C::kWaitFirst>();
-    else wait_vmcnt<C::kWaitSteady>();
-    lds_barrier();  // chunk c is in LDS; every wave is done with chunk c - 1
-    {
-      const int64_t cn = c + kFStages - 1;
-      issue(cn < NT ? cn : NT - 1, (int)(cn % kFStages));
+    if (state_wave) {
+      if (c < kFStages - 1) wait_vmcnt<C::kWaitFirst>();
+      else wait_vmcnt<C::kWaitSteady>();
     }
+    lds_barrier();  // A: chunk c is in LDS; every wave is done with chunk c - 1
     const char* tk = stage_k(s);
-    const char* tw = stage_w(s);
     const char* tq = stage_q(s);
-    const char* tu = stage_u(s);
     const float* gs = HAS_G ? stage_g(s) + wq * kBT : nullptr;
 
-    // S as the B operand: pairs of 16-row tiles, paired contraction order.
-    bf16x8 sb[C::KB / 2];
-#pragma unroll
-    for (int s2 = 0; s2 < C::KB / 2; ++s2) {
-      const float f[8] = {S[2 * s2][0], S[2 * s2][1], S[2 * s2][2], S[2 * s2][3],
-                          S[2 * s2 + 1][0], S[2 * s2 + 1][1], S[2 * s2 + 1][2], S[2 * s2 + 1][3]};
-      sb[s2] = to_bf16x8(f);
-    }
-    // rows x S for a 16-row block of a [64 x K] tile (w or q).
-    auto rows_times_S = [&](const char* tile, int ib) {
-      f32x4 acc = zero4();
-      const int row = 16 * ib + li;
-#pragma unroll
-      for (int s2 = 0; s2 < C::KB / 2; ++s2) {
-        const int e0 = 32 * s2 + 4 * grp;
-        const bf16x4 a0 = *reinterpret_cast<const bf16x4*>(tile + hl::tile_off(row, e0, C::kRowK));
-        const bf16x4 a1 = *reinterpret_cast<const bf16x4*>(tile + hl::tile_off(row, e0 + 16, C::kRowK));
-        acc = mfma16x16x32(concat(a0, a1), sb[s2], acc);
+    f32x4 vn[4];    // state waves: v_new rows j = 16 jb + 4 grp + r of column 16 wq + li
+    bf16x8 vp[2];   // state waves: v_new as bf16 B-operand pairs
+    if (state_wave) {
+      {
+        const int64_t cn = c + kFStages - 1;
+        issue(cn < NT ? cn : NT - 1, (int)(cn % kFStages));
       }
-      return acc;
-    };
-
-    // v_new rows j = 16 jb + 4 grp + r of column 16 wq + li.
-    f32x4 vn[4];
+      // S as the B operand (pairs of 16-row tiles), also handed to the output wave.
+      bf16x8 sb[KB2];
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(
-          tu + hl::tile_off(16 * jb + 4 * grp + (li >> 2), 16 * wq + 4 * (li & 3), C::kRowU)));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
-      vn[jb] -= rows_times_S(tw, jb);
-    }
-    if constexpr (STORE_VN) {
-      bf16* vb = vnew + ((b * T + c * kBT) * H + hh) * V;
-#pragma unroll
-      for (int jb = 0; jb < 4; ++jb) store_rows(vb, jb, vn[jb]);
-    }
-    // v_new as the B operand of the local term (paired order over j).
-    bf16x8 vb16[2];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const float f[8] = {vn[2 * s2][0], vn[2 * s2][1], vn[2 * s2][2], vn[2 * s2][3],
-                          vn[2 * s2 + 1][0], vn[2 * s2 + 1][1], vn[2 * s2 + 1][2], vn[2 * s2 + 1][3]};
-      vb16[s2] = to_bf16x8(f);
-    }
-
-    // Output, one 16-row query block at a time.
-    bf16* ob = o + ((b * T + c * kBT) * H + hh) * V;
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      f32x4 acc = rows_times_S(tq, ib);  // q S
-      if constexpr (HAS_G) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] *= fast_exp(gs[16 * ib + 4 * grp + r]);
+      for (int s2 = 0; s2 < KB2; ++s2) {
+        const float f[8] = {S[2 * s2][0], S[2 * s2][1], S[2 * s2][2], S[2 * s2][3],
+                            S[2 * s2 + 1][0], S[2 * s2 + 1][1], S[2 * s2 + 1][2], S[2 * s2 + 1][3]};
+        sb[s2] = to_bf16x8(f);
+        ls[s2 * 64] = sb[s2];
       }
-      // Scores P^T[j][i] for key blocks jb <= ib, i = 16 ib + li.
-      f32x4 pt[4];
+      // P1: v_new = u - w S.
+      const char* tw = stage_w(s);
+      const char* tu = stage_u(s);
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
-        pt[jb] = zero4();
-        if (jb > ib) continue;
+        const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(
+            tu + hl::tile_off(16 * jb + 4 * grp + (li >> 2), 16 * wq + 4 * (li & 3), C::kRowU)));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
+        vn[jb] -= rows_times_S(tw, jb, sb);
+      }
+      if constexpr (STORE_VN) {
+        bf16* vb = vnew + ((b * T + c * kBT) * H + hh) * V;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) store_rows(vb, jb, vn[jb]);
+      }
+      // v_new as the B operand of the local term (paired order over j), to the output wave.
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const float f[8] = {vn[2 * s2][0], vn[2 * s2][1], vn[2 * s2][2], vn[2 * s2][3],
+                            vn[2 * s2 + 1][0], vn[2 * s2 + 1][1], vn[2 * s2 + 1][2], vn[2 * s2 + 1][3]};
+        vp[s2] = to_bf16x8(f);
+        lv[s2 * 64] = vp[s2];
+      }
+    } else {
+      // Scores, once per workgroup: P[i][j] = (q_i . k_j) e^{g_i - g_j} for
+      // j <= i (0 above the diagonal), as bf16 rows of lp.  The ten 16 x 16
+      // blocks (ib, jb <= ib) are shared out 3 / 3 / 2 / 2 over the output
+      // waves; the accumulator of block (ib, jb) holds
+      // P^T[j = 16 jb + 4 grp + r][i = 16 ib + li], so each lane stores 4
+      // consecutive j of row i as one 8-byte write.
+      const uint32_t blocks = wq == 0 ? 0x0E0D0Cu : wq == 1 ? 0x0A0908u : wq == 2 ? 0xFF040Fu : 0xFF0005u;
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const int id = (int)((blocks >> (8 * t)) & 0xFF);
+        if (id == 0xFF) break;
+        const int ib = id >> 2, jb = id & 3;
+        f32x4 pt = zero4();
 #pragma unroll
         for (int s2 = 0; s2 < K / 32; ++s2) {
           const bf16x8 kf = load8(reinterpret_cast<const bf16*>(tk + hl::tile_off(16 * jb + li, 32 * s2 + 8 * grp, C::kRowK)));
           const bf16x8 qf = load8(reinterpret_cast<const bf16*>(tq + hl::tile_off(16 * ib + li, 32 * s2 + 8 * grp, C::kRowK)));
-          pt[jb] = mfma16x16x32(kf, qf, pt[jb]);
+          pt = mfma16x16x32(kf, qf, pt);
         }
         const int i = 16 * ib + li;
+        bf16x4 pv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = 16 * jb + 4 * grp + r;
           float gate = 1.f;
           if constexpr (HAS_G) gate = fast_exp(gs[i] - gs[j]);
-          pt[jb][r] = (j <= i) ? pt[jb][r] * gate : 0.f;
+          pv[r] = (bf16)((j <= i) ? pt[r] * gate : 0.f);
         }
+        *reinterpret_cast<bf16x4*>(lp + hl::tile_off(i, 16 * jb + 4 * grp, 128)) = pv;
       }
-      // Local term: A = P[i][j] (the P^T pairs), B = v_new (pairs), paired order over j.
-      f32x4 loc = zero4();
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        if (2 * s2 > ib) continue;
-        const float f[8] = {pt[2 * s2][0], pt[2 * s2][1], pt[2 * s2][2], pt[2 * s2][3],
-                            pt[2 * s2 + 1][0], pt[2 * s2 + 1][1], pt[2 * s2 + 1][2], pt[2 * s2 + 1][3]};
-        loc = mfma16x16x32(to_bf16x8(f), vb16[s2], loc);
-      }
-      store_rows(ob, ib, (acc + loc) * scale);
     }
+    lds_barrier();  // M: P, the S pairs and the v_new pairs of chunk c are in LDS
 
-    // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
-    bf16x8 vh[2];
-    float decay = 1.f;
-    if constexpr (HAS_G) {
-      const float gl = gs[kBT - 1];
-      decay = fast_exp(gl);
+    if (state_wave) {
+      // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
+      bf16x8 vh[2];
+      float decay = 1.f;
+      if constexpr (HAS_G) {
+        const float gl = gs[kBT - 1];
+        decay = fast_exp(gl);
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        float f[8];
+        for (int s2 = 0; s2 < 2; ++s2) {
+          float f[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j0 = 32 * s2 + 4 * grp + r;
-          f[r] = vn[2 * s2][r] * fast_exp(gl - gs[j0]);
-          f[4 + r] = vn[2 * s2 + 1][r] * fast_exp(gl - gs[j0 + 16]);
+          for (int r = 0; r < 4; ++r) {
+            const int j0 = 32 * s2 + 4 * grp + r;
+            f[r] = vn[2 * s2][r] * fast_exp(gl - gs[j0]);
+            f[4 + r] = vn[2 * s2 + 1][r] * fast_exp(gl - gs[j0 + 16]);
+          }
+          vh[s2] = to_bf16x8(f);
         }
-        vh[s2] = to_bf16x8(f);
+      } else {
+        vh[0] = vp[0];
+        vh[1] = vp[1];
+      }
+#pragma unroll
+      for (int kb = 0; kb < C::KB; ++kb) {
+        if constexpr (HAS_G) S[kb] *= decay;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int col = 16 * kb + 4 * (li & 3);
+          const bf16x4 a = ds_read_tr16(reinterpret_cast<const bf16*>(
+              tk + hl::tile_off(32 * s2 + 4 * grp + (li >> 2), col, C::kRowK)));
+          const bf16x4 bq = ds_read_tr16(reinterpret_cast<const bf16*>(
+              tk + hl::tile_off(32 * s2 + 16 + 4 * grp + (li >> 2), col, C::kRowK)));
+          S[kb] = mfma16x16x32(concat(a, bq), vh[s2], S[kb]);
+        }
       }
     } else {
-      vh[0] = vb16[0];
-      vh[1] = vb16[1];
-    }
+      // Output, one 16-row query block at a time: o = scale (e^{g_i} q S + P v_new).
+      bf16x8 sb[KB2];
 #pragma unroll
-    for (int kb = 0; kb < C::KB; ++kb) {
-      if constexpr (HAS_G) S[kb] *= decay;
+      for (int s2 = 0; s2 < KB2; ++s2) sb[s2] = ls[s2 * 64];
+      const bf16x8 vb16[2] = {lv[0], lv[64]};
+      bf16* ob = o + ((b * T + c * kBT) * H + hh) * V;
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const int col = 16 * kb + 4 * (li & 3);
-        const bf16x4 a = ds_read_tr16(reinterpret_cast<const bf16*>(
-            tk + hl::tile_off(32 * s2 + 4 * grp + (li >> 2), col, C::kRowK)));
-        const bf16x4 bq = ds_read_tr16(reinterpret_cast<const bf16*>(
-            tk + hl::tile_off(32 * s2 + 16 + 4 * grp + (li >> 2), col, C::kRowK)));
-        S[kb] = mfma16x16x32(concat(a, bq), vh[s2], S[kb]);
+      for (int ib = 0; ib < 4; ++ib) {
+        f32x4 acc = rows_times_S(tq, ib, sb);  // q S
+        if constexpr (HAS_G) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] *= fast_exp(gs[16 * ib + 4 * grp + r]);
+        }
+        // Local term: A = P[i][j] rows of lp, B = v_new (pairs), paired order
+        // over j; key blocks above the diagonal block contribute zero.
+        f32x4 loc = zero4();
+        const int i = 16 * ib + li;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          if (2 * s2 > ib) continue;
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(lp + hl::tile_off(i, 32 * s2 + 4 * grp, 128));
+          bf16x4 hi = {};
+          if (2 * s2 + 1 <= ib) hi = *reinterpret_cast<const bf16x4*>(lp + hl::tile_off(i, 32 * s2 + 16 + 4 * grp, 128));
+          loc = mfma16x16x32(concat(lo, hi), vb16[s2], loc);
+        }
+        store_rows(ob, ib, (acc + loc) * scale);
       }
     }
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS when it exits
 
-  if (ht) {
+  if (state_wave && ht) {
 #pragma unroll
     for (int kb = 0; kb < C::KB; ++kb)
 #pragma unroll
