@@ -50,6 +50,7 @@ constexpr int kBT = 64;
 constexpr int kFBV = 64;        // V-tile width
 constexpr int kFThreads = 512;  // 4 state + 4 output wavefronts
 constexpr int kFStages = 2;
+constexpr bool kFPrefetch = true;  // L2 prefetch of the chunk after the one in flight
 
 template <int K, bool HAS_G, bool STORE_VN>
 struct FCfg {
@@ -63,13 +64,18 @@ struct FCfg {
   static constexpr int kPBytes = kBT * kBT * 2;   // the chunk's scores P, bf16
   static constexpr int kSBytes = 4 * (KB / 2) * 64 * 16;  // S handed over as bf16 B-operand pairs
   static constexpr int kVBytes = 4 * 2 * 64 * 16;         // v_new handed over the same way
-  static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes;
+  static constexpr int kTrash = 256;                      // landing slot of the L2 prefetch DMAs
+  static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes + kTrash;
   static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per state wave per k / w / q tile
   static constexpr int kUDma = kTileU / 1024 / 4;
   static constexpr int kDma = 3 * kKDma + kUDma + (HAS_G ? 1 : 0);
   static constexpr int kStores = STORE_VN ? 4 : 0;  // v_new row tiles per state wave
-  static constexpr int kWaitFirst = (kFStages - 2) * kDma;
-  static constexpr int kWaitSteady = (kFStages - 1) * kStores + (kFStages - 2) * kDma;
+  static constexpr int kPf = kFPrefetch ? 4 : 0;    // L2 prefetch DMAs per state wave per chunk
+  // Ops a state wave issues after the DMA of chunk c before it waits for it:
+  // the prefetch of chunk c + 1 (and, from c = 1 on, the stores of chunk c - 1).
+  static constexpr int kWaitFirst = kPf;
+  static constexpr int kWaitSteady = kPf + kStores;
+  static_assert(kFStages == 2, "the wait counts assume double buffering");
   static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
   static_assert(kLds <= 160 * 1024, "LDS budget");
   static_assert(kWaitSteady <= 63, "vmcnt range");
@@ -117,6 +123,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   // Hand-over slots, lane-major: 16 bytes per lane per B-operand pair.
   bf16x8* const ls = reinterpret_cast<bf16x8*>(lp + C::kPBytes) + wq * KB2 * 64 + lane;
   bf16x8* const lv = reinterpret_cast<bf16x8*>(lp + C::kPBytes + C::kSBytes) + wq * 2 * 64 + lane;
+  char* const ltrash = lp + C::kPBytes + C::kSBytes + C::kVBytes;
 
   // Global geometry in bytes.  Token t of chunk c, head hh: ((b T + 64 c + t) H + hh) D.
   const int64_t tsk = H * K * 2, tsv = H * V * 2;
@@ -160,6 +167,54 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     }
   };
 
+  // L2 prefetch of chunk cc (state waves): one 4-byte DMA per 64-byte line of
+  // the chunk's tiles, landing in a scratch LDS slot whose contents are never
+  // read, so the DMA of that chunk one iteration later finds its lines in L2.
+  // Waves 0, 1, 2 cover the k, w, q rows (up to 256 lines each), wave 3 the
+  // u rows of the V-tile and the gates; surplus lanes repeat lines.
+  uint32_t pfo[4];
+  {
+    constexpr int kLinesK = C::kRowK / 64, kLinesU = C::kRowU / 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int L = i * 64 + lane;
+      if (wq < 3) {
+        pfo[i] = (uint32_t)(((L / kLinesK) % kBT) * tsk + (L % kLinesK) * 64);
+      } else {
+        const int Lu = (i & 1) * 64 + lane;
+        pfo[i] = (HAS_G && i >= 2) ? goff : (uint32_t)(((Lu / kLinesU) % kBT) * tsv + (Lu % kLinesU) * 64);
+      }
+    }
+  }
+  // Per-wave prefetch sources (instructions 0-1 from pfa, 2-3 from pfb), chunk strides.
+  const char* pfa;
+  const char* pfb;
+  int64_t pfsa, pfsb;
+  if (wq < 3) {
+    pfa = (wq == 0 ? reinterpret_cast<const char*>(k) : wq == 1 ? reinterpret_cast<const char*>(w)
+                                                                : reinterpret_cast<const char*>(q)) + kc0;
+    pfb = pfa;
+    pfsa = pfsb = kcs;
+  } else {
+    pfa = reinterpret_cast<const char*>(u) + uc0;
+    pfsa = ucs;
+    pfb = HAS_G ? reinterpret_cast<const char*>(g) + gc0 : pfa;
+    pfsb = HAS_G ? gcs : ucs;
+  }
+  pfa = reinterpret_cast<const char*>(uniform_ptr(pfa));
+  pfb = reinterpret_cast<const char*>(uniform_ptr(pfb));
+  auto prefetch = [&](int64_t cc) {
+    if constexpr (kFPrefetch) {
+      const uint32_t lt = __builtin_amdgcn_readfirstlane(lds_address(ltrash));
+      const char* a = pfa + cc * pfsa;
+      const char* bb = pfb + cc * pfsb;
+      dma_b32(a, pfo[0], lt);
+      dma_b32(a, pfo[1], lt);
+      dma_b32(bb, pfo[2], lt);
+      dma_b32(bb, pfo[3], lt);
+    }
+  };
+
   // rows x S for a 16-row block of a [64 x K] tile (w or q): A = tile rows,
   // B = the S pairs sbv, paired contraction order.
   auto rows_times_S = [&](const char* tile, int ib, const bf16x8* sbv) {
@@ -197,7 +252,10 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       S[kb][r] = (state_wave && h0) ? h0[st_base + (int64_t)(16 * kb + 4 * grp + r) * V + ncol] : 0.f;
   wait_vmcnt<0>();  // retire the h0 loads before the counted loop
 
-  if (state_wave && NT > 0) issue(0, 0);
+  if (state_wave && NT > 0) {
+    issue(0, 0);
+    prefetch(NT > 1 ? 1 : 0);
+  }
   for (int64_t c = 0; c < NT; ++c) {
     const int s = (int)(c % kFStages);
     if (state_wave) {
@@ -215,6 +273,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       {
         const int64_t cn = c + kFStages - 1;
         issue(cn < NT ? cn : NT - 1, (int)(cn % kFStages));
+        prefetch(cn + 1 < NT ? cn + 1 : NT - 1);
       }
       // S as the B operand (pairs of 16-row tiles), also handed to the output wave.
       bf16x8 sb[KB2];

@@ -25,9 +25,22 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(size_t)(lds_void_t*)p;
 }
 
+// A wave-uniform pointer, moved to scalar registers.  The compiler cannot
+// always prove a pointer uniform (a select between kernel arguments by a
+// uniform wave index, for example) and would hand the scalar operand of the
+// instructions below a vector register; for a value already in scalar
+// registers this folds away.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+
 // global -> LDS, 16 bytes per lane: lane i's bytes [base + voff_i, +16) land at
 // LDS [lds + 16 i, +16).  M0 (the LDS base register) is restored afterwards.
 __device__ __forceinline__ void dma_b128(const void* base, uint32_t voff, uint32_t lds) {
+  base = uniform_ptr(base);
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
@@ -43,6 +56,7 @@ __device__ __forceinline__ void dma_b128(const void* base, uint32_t voff, uint32
 // global -> LDS, 4 bytes per lane: lane i's bytes [base + voff_i, +4) land at
 // LDS [lds + 4 i, +4).
 __device__ __forceinline__ void dma_b32(const void* base, uint32_t voff, uint32_t lds) {
+  base = uniform_ptr(base);
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
