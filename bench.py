@@ -201,7 +201,7 @@ def work_build_A(B, T, H, K, eb=2):
 
 def extension_timings(torch, inp, conv_in, iters: int = 10):
     """The kernels beyond the four (WY matrix, gate cumsum, channels-last conv,
-    conv decode step, fused h + o, the whole chunked forward) at config-4
+    conv decode step, fused WY, fused h + o, the whole chunked forward) at config-4
     sizes: HIP events around ``iters`` back-to-back launches after one warm-up."""
     from theorem_amd import chain
     from theorem_amd.kernels import causal_conv1d, recompute_w_u
@@ -227,6 +227,10 @@ def extension_timings(torch, inp, conv_in, iters: int = 10):
     ww, uu = recompute_w_u.custom_kernel(recompute_w_u.Data(
         k=inp["k"], v=inp["v"], beta=inp["beta"], A=inp["A"], g=inp["g"], B=B, T=T, H=H, K=K, V=V))
     N = B * T * H
+    cases["wy_fwd"] = (
+        lambda: chain.wy_fwd(inp["k"], inp["v"], inp["beta"], inp["g"], sign=+1),
+        N * (K * 2 + V * 2 + 8) + N * (K * 2 + V * 2),
+        f"({B},{T},{H},{K},{V}) bf16: A-builder + recompute_w_u fused, A kept on chip")
     cases["chunk_gated_delta_fwd"] = (
         lambda: chain.chunk_fwd_fused(inp["q"], inp["k"], ww, uu, inp["g"], inp["scale"], None, True),
         N * (3 * K * 2 + V * 2 + 4) + N * V * 2 + B * H * K * V * 4,
@@ -234,8 +238,8 @@ def extension_timings(torch, inp, conv_in, iters: int = 10):
     cases["chunk_gated_delta_rule_fwd"] = (
         lambda: chain.chunk_gated_delta_rule_fwd(inp["q"], inp["k"], inp["v"], inp["beta"], inp["g"], inp["scale"],
                                                  output_final_state=True),
-        work_build_A(B, T, H, K) + work_wu(B, T, H, K, V)[0] + N * (3 * K * 2 + V * 2 + 4) + N * V * 2,
-        "the whole chunked forward from (q, k, v, beta, g): A-builder, recompute_w_u, fused h + o")
+        N * (K * 2 + V * 2 + 8) + N * (K * 2 + V * 2) + N * (3 * K * 2 + V * 2 + 4) + N * V * 2 + B * H * K * V * 4,
+        "the whole chunked forward from (q, k, v, beta, g): fused WY (A, w, u), fused h + o")
     out = {}
     for name, (fn, by, shape) in cases.items():
         fn()
@@ -264,7 +268,7 @@ def main() -> int:
     ap.add_argument("--no-ext", action="store_true", help="skip the extension kernels (A-builder, gate cumsum, ...)")
     ap.add_argument("--small", action="store_true", help="1/8-size workload (quick check)")
     ap.add_argument("--only", choices=["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o", "wy_build_A",
-                                        "chunk_gated_delta_fwd"],
+                                        "chunk_gated_delta_fwd", "wy_fwd"],
                     help="run only this kernel of the step (for per-kernel rocprofv3 counter runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (rocprofv3 counter calibration)")
@@ -335,6 +339,7 @@ def main() -> int:
             "chunk_fwd_o": lambda: chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=vn, g=g, h=h, scale=scale)),
             "wy_build_A": lambda: recompute_w_u.build_A(k, beta, g, sign=+1),
             "chunk_gated_delta_fwd": lambda: chain.chunk_fwd_fused(q, k, w, u, g, scale, None, True),
+            "wy_fwd": lambda: chain.wy_fwd(k, v, beta, g, sign=+1),
         }[args.only]
         for _ in range(args.warmup + args.steps):
             run()

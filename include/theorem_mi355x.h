@@ -198,6 +198,20 @@ int thm_wy_build_A(const void* k, const void* beta, const void* g, void* A,
                    int32_t chunk_size, int32_t k_dtype, int32_t sign, void* stream);
 
 /*
+ * Fused WY forward: the WY matrix A_c of thm_wy_build_A (same sign convention)
+ * and the recompute_w_u products with it, in one pass, per chunk c:
+ *   w_c = A_c (k_c * beta_c exp(g_c)),   u_c = A_c (v_c * beta_c)
+ * A is never written.  Replaces `_build_A` followed by the recompute_w_u
+ * kernel (kernels/recompute_w_u/reference.py:48-91 and :118-149) for callers
+ * that need only w and u; w and u equal thm_wy_build_A + thm_recompute_w_u_fwd.
+ *   bf16 only (kv_dtype = THM_DTYPE_BF16): k, v, w, u bf16; beta, g fp32.
+ *   g may be NULL (no gate). K, V in {64, 128}; T % 64 == 0.
+ */
+int thm_wy_fwd(const void* k, const void* v, const void* beta, const void* g, void* w, void* u,
+               int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+               int32_t chunk_size, int32_t kv_dtype, int32_t sign, void* stream);
+
+/*
  * Gate preprocessing: per 64-token chunk, the inclusive cumulative sum of the
  * per-token log decay,
  *   g[b, t, h] = sum_{t' in chunk(t), t' <= t} f(a[b, t', h]),

@@ -25,7 +25,7 @@ def declared_symbols() -> list[str]:
 def test_header_lists_entry_points():
     syms = declared_symbols()
     assert {"thm_causal_conv1d_fwd", "thm_recompute_w_u_fwd", "thm_chunk_fwd_h",
-            "thm_chunk_fwd_o", "thm_wy_build_A", "thm_chunk_local_cumsum",
+            "thm_chunk_fwd_o", "thm_wy_build_A", "thm_chunk_local_cumsum", "thm_wy_fwd",
             "thm_status_string", "thm_abi_version"} <= set(syms)
 
 
@@ -87,6 +87,20 @@ def test_build_A_and_cumsum_validation():
     assert A(kd=5) == -3 and A(K=96) == -4 and A(bt=32) == -6 and A(sign=0) == -6
     assert A(k=FAKE + 8) == -5 and A(beta=FAKE + 2) == -5
     assert A(B=0) == 0 and A(T=0) == 0
+
+    def wy(**kw):
+        a = dict(k=FAKE, v=FAKE, beta=FAKE, g=FAKE, w=FAKE, u=FAKE, B=1, T=64, H=2, K=64, V=128, bt=64,
+                 kd=1, sign=1)
+        a.update(kw)
+        return lib.thm_wy_fwd(a["k"], a["v"], a["beta"], a["g"], a["w"], a["u"], a["B"], a["T"], a["H"],
+                              a["K"], a["V"], a["bt"], a["kd"], a["sign"], None)
+
+    assert wy(k=None) == -1 and wy(v=None) == -1 and wy(beta=None) == -1 and wy(w=None) == -1 and wy(u=None) == -1
+    assert wy(T=65) == -2 and wy(H=0) == -2 and wy(B=-1) == -2 and wy(V=0) == -2
+    assert wy(kd=0) == -3 and wy(kd=5) == -3  # bf16 only
+    assert wy(K=96) == -4 and wy(V=32) == -4 and wy(bt=32) == -6 and wy(sign=2) == -6
+    assert wy(k=FAKE + 8) == -5 and wy(v=FAKE + 8) == -5 and wy(w=FAKE + 4) == -5 and wy(g=FAKE + 2) == -5
+    assert wy(B=0) == 0 and wy(T=0) == 0
 
     def cs(**kw):
         a = dict(a=FAKE, g=FAKE, B=1, T=64, H=2, bt=64, ad=0, mode=0)

@@ -126,6 +126,23 @@ def test_cfg4_fused_forward(chain):
         assert dev_ <= 1e-2 * (1 + float(ref.float().abs().max())), f"fused {what}: max |diff| {dev_:.3e}"
 
 
+def test_cfg4_wy_fwd_full(chain):
+    # The fused WY kernel at full size: bit-identical to A-builder + recompute_w_u
+    # (the same fp32 A on chip), and within tolerance of the chain's w, u (whose A
+    # is the generator's float64 inverse rounded to fp32).
+    from theorem_amd.chain import wy_fwd
+    d = chain
+    w, u = wy_fwd(d["k"], d["v"], d["beta"], d["g"], sign=+1)
+    A = recompute_w_u.build_A(d["k"], d["beta"], d["g"], sign=+1)
+    w2, u2 = recompute_w_u.custom_kernel(recompute_w_u.Data(k=d["k"], v=d["v"], beta=d["beta"], A=A,
+                                                            g=d["g"], B=B, T=T, H=H, K=K, V=V))
+    torch.cuda.synchronize()
+    assert torch.equal(w, w2) and torch.equal(u, u2), "wy_fwd differs from A-builder + recompute_w_u"
+    for what, got, ref in (("w", w, d["w"]), ("u", u, d["u"])):
+        dev_ = float((got.float() - ref.float()).abs().max())
+        assert dev_ <= 1e-2 * (1 + float(ref.float().abs().max())), f"wy_fwd {what}: max |diff| {dev_:.3e}"
+
+
 def test_cfg4_homogeneity(chain):
     # w, u are linear in A; h, v_new, final state are linear in u (zero initial
     # state); o is linear in (v, h) jointly.

@@ -153,3 +153,60 @@ def test_fused_forward_matches_two_kernels_and_oracle(dev, K, V, gate):
                                       None, scale, d["h0"], True)
     torch.cuda.synchronize()
     assert torch.equal(ht0, d["h0"])
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (64, 128), (128, 64), (128, 128)])
+@pytest.mark.parametrize("sign", [1, -1])
+@pytest.mark.parametrize("gate", ["logsigmoid", None])
+def test_wy_fwd_matches_two_kernels_and_oracle(dev, K, V, sign, gate):
+    # thm_wy_fwd = thm_wy_build_A followed by recompute_w_u with A kept on chip:
+    # the same fp32 A and the same products, so w and u agree bit for bit; and
+    # against the float64 oracle (A from the oracle's build_A).
+    B, T, H = 2, 192, 3
+    k, beta, g = _A_inputs(B, T, H, K, torch.bfloat16, gate, seed=41, dev=dev)
+    gen = torch.Generator().manual_seed(42)
+    v = torch.randn(B, T, H, V, generator=gen).to(torch.bfloat16).to(dev)
+    w, u = chain.wy_fwd(k, v, beta, g, sign=sign)
+    A = recompute_w_u.build_A(k, beta, g, sign=sign)
+    w2, u2 = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V))
+    torch.cuda.synchronize()
+    assert w.dtype == u.dtype == torch.bfloat16 and w.shape == k.shape and u.shape == v.shape
+    assert torch.equal(w, w2), f"w differs from the two-kernel path (K={K} V={V} sign={sign} gate={gate})"
+    assert torch.equal(u, u2), f"u differs from the two-kernel path (K={K} V={V} sign={sign} gate={gate})"
+    gk = np_(g) if g is not None else np.zeros((B, T, H))
+    eA = odn.build_A(np_(k), np_(beta), gk, sign=sign)
+    ew, eu = odn.recompute_w_u_ref(np_(k), np_(v), np_(beta), eA, gk)
+    assert_close(w, ew, 1e-2, 1e-2, f"w vs oracle K={K} V={V} sign={sign} gate={gate}")
+    assert_close(u, eu, 1e-2, 1e-2, f"u vs oracle K={K} V={V} sign={sign} gate={gate}")
+
+
+def test_wy_fwd_empty_and_errors(dev):
+    e = torch.empty(1, 0, 2, 64, device=dev, dtype=torch.bfloat16)
+    w, u = chain.wy_fwd(e, e, torch.empty(1, 0, 2, device=dev), None)
+    torch.cuda.synchronize()
+    assert w.shape == (1, 0, 2, 64) and u.shape == (1, 0, 2, 64)
+    z = torch.zeros(1, 64, 2, 96, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        chain.wy_fwd(z, z, torch.zeros(1, 64, 2, device=dev), None)
+    with pytest.raises(AssertionError):
+        f = torch.zeros(1, 64, 2, 64, device=dev)
+        chain.wy_fwd(f, f, torch.zeros(1, 64, 2, device=dev), None)
+
+
+def test_driver_fused_matches_unfused(dev):
+    # The driver's bf16 default (wy_fwd + chunk_fwd_fused) against its
+    # four-kernel form on the same inputs.
+    gen = torch.Generator().manual_seed(51)
+    B, T, H, K, V = 2, 256, 4, 128, 64
+    q = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16).to(dev)
+    k = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16).to(dev)
+    v = torch.randn(B, T, H, V, generator=gen).to(torch.bfloat16).to(dev)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen)).to(dev)
+    logits = torch.randn(B, T, H, generator=gen).to(dev)
+    o1, s1 = chain.chunk_gated_delta_rule_fwd(q, k, v, beta, None, K ** -0.5, output_final_state=True,
+                                              a=logits, a_logsigmoid=True)
+    o2, s2 = chain.chunk_gated_delta_rule_fwd(q, k, v, beta, None, K ** -0.5, output_final_state=True,
+                                              a=logits, a_logsigmoid=True, fused=False)
+    torch.cuda.synchronize()
+    assert_close(o1, o2, 1e-2, 1e-2, "driver o fused vs unfused")
+    assert_close(s1, s2, 1e-2, 1e-2, "driver final state fused vs unfused")

@@ -30,6 +30,7 @@ SOURCES = [
     "chunk_fwd_o.hip",
     "chunk_fwd_fused.hip",
     "wy_build_A.hip",
+    "wy_fwd.hip",
     "gates.hip",
 ]
 

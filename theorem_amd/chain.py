@@ -4,7 +4,8 @@
     (w, u) = recompute_w_u(k, v, beta, A, g)                            HIP
     (h, v_new, S) = chunk_fwd_h delta form (h[c] before chunk c)        HIP
     o      = chunk_fwd_o(q, k, v_new, g, h, scale)                      HIP
-    (the last two fused into one kernel for bf16: chunk_fwd_fused)
+    (for bf16 the first two fused into one kernel, wy_fwd, and the last
+    two into another, chunk_fwd_fused)
 
 The reference never composes its ops (each is tested alone); this is the
 forward of chunked Gated DeltaNet that the three ops are the stages of, and
@@ -12,7 +13,8 @@ it reproduces the token-by-token gated delta rule
     S_t = e^{a_t} S_{t-1};  S_t += beta_t k_t (v_t - S_t^T k_t)^T;  o_t = scale S_t^T q_t
 with g the chunk-local cumsum of a.
 
-``build_A`` (the WY matrix) is the HIP kernel thm_wy_build_A.
+``build_A`` (the WY matrix) is the HIP kernel thm_wy_build_A; ``wy_fwd`` is
+thm_wy_fwd.
 """
 from __future__ import annotations
 
@@ -41,6 +43,28 @@ def chunk_local_cumsum(a: torch.Tensor, logsigmoid: bool = False) -> torch.Tenso
 def build_A(k: torch.Tensor, beta: torch.Tensor, g: torch.Tensor | None) -> torch.Tensor:
     """A [B, T, H, 64] fp32 = per-chunk (I + strict_lower(beta_i k_i.k_j e^{g_i - g_j}))^{-1} (HIP)."""
     return recompute_w_u.build_A(k, beta, g, sign=+1)
+
+
+def wy_fwd(k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, g: torch.Tensor | None,
+           sign: int = +1) -> tuple[torch.Tensor, torch.Tensor]:
+    """(w, u) = recompute_w_u(k, v, beta, A, g) with A = build_A(k, beta, g, sign)
+    formed inside the same HIP kernel and never written (thm_wy_fwd; bf16 k, v)."""
+    B, T, H, K = k.shape
+    V = v.shape[-1]
+    assert T % BT == 0, f"T={T} must be a multiple of {BT}"
+    assert v.shape[:3] == (B, T, H) and beta.shape == (B, T, H) and (g is None or g.shape == (B, T, H))
+    assert k.dtype == v.dtype == torch.bfloat16, "the fused path is bf16-only"
+    _capi.require_device(k, v, beta, g)
+    for name, t in (("beta", beta), ("g", g)):
+        _capi.require_f32(t, name)
+    k, v, beta, g = (_capi.prep(t, n) for t, n in ((k, "k"), (v, "v"), (beta, "beta"), (g, "g")))
+    w = torch.empty_like(k)
+    u = torch.empty_like(v)
+    status = _capi.load_library().thm_wy_fwd(
+        _capi.ptr(k), _capi.ptr(v), _capi.ptr(beta), _capi.ptr(g), _capi.ptr(w), _capi.ptr(u),
+        B, T, H, K, V, BT, _capi.THM_DTYPE[torch.bfloat16], int(sign), _capi.stream_of(k))
+    _capi.check(status, "thm_wy_fwd")
+    return w, u
 
 
 def chunk_fwd_fused(q, k, w, u, g, scale: float, initial_state=None, output_final_state: bool = False,
@@ -75,9 +99,11 @@ def chunk_gated_delta_rule_fwd(q, k, v, beta, g, scale: float, initial_state=Non
                                a_logsigmoid: bool = False, fused: bool | None = None):
     """o [B, T, H, V] (dtype of q) and the final state [B, H, K, V] fp32 (or None).
 
-    bf16 inputs run the state recurrence and the output in one fused kernel
-    (``fused``, default for bf16 unless ``return_intermediates``, which needs
-    the per-chunk states h); otherwise chunk_fwd_h then chunk_fwd_o.
+    bf16 inputs run two fused kernels (``fused``, default for bf16 unless
+    ``return_intermediates``, which needs A and the per-chunk states h): wy_fwd
+    (A and w, u; unless ``A`` is given) and chunk_fwd_fused (the state
+    recurrence and the output); otherwise build_A, recompute_w_u, chunk_fwd_h,
+    chunk_fwd_o.
     ``g`` is the chunk-local cumulative log decay [B, T, H] fp32 (or None: no
     gate).  Alternatively pass the per-token log decay ``a`` (g = None): g is
     then formed on the GPU by chunk_local_cumsum(a), of log(sigmoid(a)) when
@@ -87,11 +113,15 @@ def chunk_gated_delta_rule_fwd(q, k, v, beta, g, scale: float, initial_state=Non
     if a is not None:
         assert g is None, "pass either g or a"
         g = chunk_local_cumsum(a, logsigmoid=a_logsigmoid)
-    if A is None:
-        A = build_A(k, beta, g)
-    w, u = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V))
     if fused is None:
         fused = k.dtype == torch.bfloat16 and not return_intermediates
+    if fused and A is None:
+        w, u = wy_fwd(k, v, beta, g, sign=+1)
+    else:
+        if A is None:
+            A = build_A(k, beta, g)
+        w, u = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g,
+                                                              B=B, T=T, H=H, K=K, V=V))
     if fused:
         o, _, ht = chunk_fwd_fused(q, k, w, u, g, scale, initial_state, output_final_state)
         return o, ht

@@ -27,37 +27,16 @@
 // HBM traffic per tile: k, beta, g read once, A written once.
 #include <type_traits>
 
-#include "mfma.h"
+#include "wy_blocks.h"
 
 namespace thm {
 namespace {
 
-constexpr int kBT = 64;
-constexpr int kBP = 17;             // LDS pitch (floats) of a 16x16 block
-constexpr int kBlk = 16 * kBP;      // floats per block
+using wy::blk;
+using wy::kBlk;
+using wy::kBP;
+constexpr int kBT = wy::kBT;
 constexpr int kABThreads = 256;
-
-// Packed index of lower block (i, j), j <= i < 4.
-__host__ __device__ constexpr int blk(int i, int j) { return i * (i + 1) / 2 + j; }
-
-__device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-// acc += P Q for 16x16 blocks P, Q in LDS (pitch kBP): lane (g, l) feeds
-// P[l][4q + g] and Q[4q + g][l] at k-step q; acc[r] = row 4g + r, column l.
-__device__ __forceinline__ f32x4 block_mm(const float* P, const float* Q, f32x4 acc) {
-  const int lane = lane_id(), g = lane >> 4, l = lane & 15;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) acc = mfma16x16x4f32(P[l * kBP + 4 * q + g], Q[(4 * q + g) * kBP + l], acc);
-  return acc;
-}
-
-__device__ __forceinline__ void block_put(float* D, f32x4 acc, float sgn) {
-  const int lane = lane_id(), g = lane >> 4, l = lane & 15;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) D[(4 * g + r) * kBP + l] = sgn * acc[r];
-}
 
 template <typename IT, int K, int SIGN>
 __global__ void __launch_bounds__(kABThreads)
@@ -106,74 +85,10 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
   }
   lds_barrier();
 
-  // 2. L blocks: wave w forms the lower blocks p = w, w + 4, w + 8 of the packed
-  //    order (compile-time block indices, so the fragments stay in registers).
-#pragma unroll
-  for (int p = 0; p < 10; ++p) {
-    if ((p & 3) != wv) continue;  // wave-uniform
-    constexpr int kIb[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
-    const int ib = kIb[p], jb = p - ib * (ib + 1) / 2;
-    f32x4 acc = zero4();
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      acc = mfma16x16x32(fh[ib][s], fh[jb][s], acc);
-      if constexpr (kSplit) {
-        acc = mfma16x16x32(fh[ib][s], fl[jb][s], acc);
-        acc = mfma16x16x32(fl[ib][s], fh[jb][s], acc);
-      }
-    }
-    const int j = 16 * jb + li;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * ib + 4 * grp + r;
-      Lb[p * kBlk + (4 * grp + r) * kBP + li] =
-          (j < i) ? (float)SIGN * sb[i] * acc[r] * fast_exp(sg[i] - sg[j]) : 0.f;
-    }
-  }
+  // 2. L blocks; 3.-4. X = (I + L)^{-1}.
+  wy::form_L<SIGN, KS, kSplit>(fh, fl, sb, sg, Lb, wv);
   lds_barrier();
-
-  // 3. Diagonal inverses: wave w, lane c < 16 owns column c of X_ww.
-  {
-    const float* L = Lb + blk(wv, wv) * kBlk;
-    float* X = Xb + blk(wv, wv) * kBlk;
-    if (lane < 16) {
-      float x[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float a0 = (r == lane) ? 1.f : 0.f, a1 = 0.f;
-#pragma unroll
-        for (int s = 0; s < r; ++s) {
-          if (s & 1) a1 = fmaf(-L[r * kBP + s], x[s], a1);
-          else a0 = fmaf(-L[r * kBP + s], x[s], a0);
-        }
-        x[r] = a0 + a1;
-        X[r * kBP + lane] = x[r];
-      }
-    }
-  }
-  lds_barrier();
-
-  // 4. Off-diagonal blocks by distance d = i - j: blocks (j + d, j), one wave each.
-#pragma unroll
-  for (int d = 1; d < 4; ++d) {
-    const int j = wv, i = wv + d;
-    const bool active = i < 4;  // wave-uniform
-    if (active) {
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int m = 0; m < 3; ++m) {
-        const int mm = j + m;
-        if (mm < i) acc = block_mm(Lb + blk(i, mm) * kBlk, Xb + blk(mm, j) * kBlk, acc);
-      }
-      block_put(Tb + wv * kBlk, acc, 1.f);
-    }
-    lds_barrier();
-    if (active) {
-      const f32x4 acc = block_mm(Xb + blk(i, i) * kBlk, Tb + wv * kBlk, zero4());
-      block_put(Xb + blk(i, j) * kBlk, acc, -1.f);
-    }
-    lds_barrier();
-  }
+  wy::invert_L(Lb, Xb, Tb, wv);
 
   // 5. A_c rows: thread (r = q / 16, chunk j4 = q % 16) writes A[r][4 j4 .. + 3].
   float* out = A + (tok0 * H + h) * kBT;

@@ -1,0 +1,194 @@
+// Fused WY forward of the Gated DeltaNet chunk forward for MI355X (gfx950):
+// per chunk c of 64 tokens,
+//   A_c = (I + sign M)^{-1},  M[i][j] = beta_i (k_i . k_j) e^{g_i - g_j}  (j < i),
+//   w_c = A_c (k_c * beta_c e^{g_c}),   u_c = A_c (v_c * beta_c),
+// i.e. the A-builder (wy_build_A.hip; the reference's `_build_A`,
+// kernels/recompute_w_u/reference.py:48-91) followed by recompute_w_u
+// (recompute_w_u.hip; reference.py:118-149) in one kernel, so A never travels
+// through HBM (its fp32 write and read are half of the two kernels' bytes).
+//
+// One workgroup (4 wavefronts) per (b, chunk, head) tile, head fastest:
+//   1. k fragments (16-byte row loads, every wave all 64 rows), beta and g;
+//   2. the L blocks (wy_blocks.h); then the [k | v] tile loads are issued
+//      into registers (the k rows hit L2), in flight during the inversion;
+//   3. X = A_c = (I + L)^{-1}, blocked (wy_blocks.h);
+//   4. wave wv forms its scaled A operands A'[t][j] (t = 16 wv + li) from X:
+//      A diag(beta e^g) for w and A diag(beta) for u, each split into bf16
+//      hi + lo, as recompute_w_u does with A read from HBM;
+//   5. barrier; the [k | v] tile is staged in LDS over the inversion's blocks;
+//      barrier;
+//   6. D[n][t] = sum_j X[j][n] A'[t][j] on v_mfma_f32_16x16x32_bf16 (X^T
+//      fragments by ds_read_b64_tr_b16), one 8-byte bf16 store per lane.
+// A is the same fp32 value the A-builder writes, and the products are
+// recompute_w_u's, so w and u equal the two-kernel path's bit for bit.
+// bf16 inputs only.  HBM traffic per tile: k, v, beta, g read once, w, u
+// written once.
+#include "wy_blocks.h"
+
+namespace thm {
+namespace {
+
+using wy::blk;
+using wy::kBlk;
+using wy::kBP;
+constexpr int kBT = wy::kBT;
+constexpr int kWyThreads = 256;
+
+template <int K, int V>
+struct WyCfg {
+  static constexpr int kN = K + V;
+  static constexpr int kPitch = kN + 8;  // [k | v] tile row pitch, bf16 elements (16-byte pad)
+  static constexpr int kTileBytes = kBT * kPitch * 2;
+  static constexpr int kInvBytes = wy::kLdsFloats * 4;
+  static constexpr int kUnion = kTileBytes > kInvBytes ? kTileBytes : kInvBytes;
+  static constexpr int kNB = kN / 16;
+  static constexpr int kCPR = kN / 8;                      // 16-byte chunks per row
+  static constexpr int kLoads = kBT * kCPR / kWyThreads;   // per thread
+  static constexpr int KS = K / 32;
+  static_assert(kBT * kCPR % kWyThreads == 0, "staging must divide evenly");
+};
+
+template <int K, int V, int SIGN>
+__global__ void __launch_bounds__(kWyThreads)
+wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
+              const float* __restrict__ beta, const float* __restrict__ g, bf16* __restrict__ w,
+              bf16* __restrict__ u, int64_t T, int64_t H, int64_t NT) {
+  using C = WyCfg<K, V>;
+  constexpr int KS = C::KS;
+  __shared__ __attribute__((aligned(16))) char lds[C::kUnion];
+  __shared__ float sb[kBT], sg[kBT];
+  float* const Lb = reinterpret_cast<float*>(lds);  // L = sign M, lower blocks
+  float* const Xb = Lb + 10 * kBlk;                  // X = A_c, lower blocks
+  float* const Tb = Xb + 10 * kBlk;                  // per-level partial products
+  bf16* const xs = reinterpret_cast<bf16*>(lds);    // [k | v] tile, after the inversion
+
+  const int64_t tile = blockIdx.x;
+  const int64_t h = tile % H;
+  const int64_t bc = tile / H;
+  const int64_t c = bc % NT;
+  const int64_t b = bc / NT;
+  const int64_t tok0 = b * T + c * kBT;
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
+  const int lane = tid & 63;
+  const int grp = lane >> 4, li = lane & 15;
+
+  // 1. k fragments: fh[tb][s] = k[tok0 + 16 tb + li][32 s + 8 grp .. + 7].
+  bf16x8 fh[4][KS], fl[4][1];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const bf16* row = k + ((tok0 + 16 * tb + li) * H + h) * K + 8 * grp;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) fh[tb][s] = load8(row + 32 * s);
+  }
+  if (tid < kBT) {
+    sb[tid] = beta[(tok0 + tid) * H + h];
+    sg[tid] = g ? g[(tok0 + tid) * H + h] : 0.f;
+  }
+  lds_barrier();
+
+  // 2. L blocks, then the [k | v] tile loads (thread q: row q / kCPR, chunk q % kCPR).
+  wy::form_L<SIGN, KS, false>(fh, fl, sb, sg, Lb, wv);
+  u32x4 xr[C::kLoads];
+#pragma unroll
+  for (int it = 0; it < C::kLoads; ++it) {
+    const int q = tid + it * kWyThreads;
+    const int j = q / C::kCPR;
+    const int col = (q - j * C::kCPR) * 8;
+    const int64_t row = (tok0 + j) * H + h;
+    xr[it] = ldg16(col < K ? (const void*)(k + row * K + col) : (const void*)(v + row * V + (col - K)));
+  }
+  lds_barrier();
+
+  // 3. X = (I + L)^{-1}.
+  wy::invert_L(Lb, Xb, Tb, wv);
+
+  // 4. Scaled A operands: A'[t][j], t = 16 wv + li, j = 32 s + 8 grp + 0..7,
+  //    in X's block (wv, jb = 2 s + grp / 2), columns 8 (grp & 1) + 0..7.
+  bf16x8 awh[2], awl[2], auh[2], aul[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int jb = 2 * s + (grp >> 1);
+    const float* X = Xb + blk(wv, jb < wv ? jb : wv) * kBlk + li * kBP + 8 * (grp & 1);
+    float fw[8], fu[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = 32 * s + 8 * grp + i;
+      const float a = (jb <= wv) ? X[i] : 0.f;
+      fu[i] = a * sb[j];
+      fw[i] = fu[i] * fast_exp(sg[j]);
+    }
+    split_bf16x8(fw, awh[s], awl[s]);
+    split_bf16x8(fu, auh[s], aul[s]);
+  }
+
+  // 5. Stage the tile over the inversion's blocks.
+  lds_barrier();  // every wave has read its A operands
+#pragma unroll
+  for (int it = 0; it < C::kLoads; ++it) {
+    const int q = tid + it * kWyThreads;
+    const int j = q / C::kCPR;
+    const int col = (q - j * C::kCPR) * 8;
+    *reinterpret_cast<u32x4*>(xs + j * C::kPitch + col) = xr[it];
+  }
+  lds_barrier();
+
+  // 6. D[n][t] = sum_j X[j][n] A'[t][j]; lane holds features 16 nb + 4 grp .. + 3 of token t.
+  const int64_t trow = (tok0 + 16 * wv + li) * H + h;
+#pragma unroll
+  for (int nb = 0; nb < C::kNB; ++nb) {
+    const bool is_w = 16 * nb < K;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int r0 = tr_row_natural(32 * s, 0), r1 = tr_row_natural(32 * s, 1);
+      const bf16x8 xh = frag_tr(xs, C::kPitch, r0, r1, 16 * nb);
+      acc = mfma16x16x32(xh, is_w ? awh[s] : auh[s], acc);
+      acc = mfma16x16x32(xh, is_w ? awl[s] : aul[s], acc);
+    }
+    const int n = 16 * nb + 4 * grp;
+    if (is_w) store4(w + trow * K + n, acc);
+    else store4(u + trow * V + (n - K), acc);
+  }
+}
+
+template <int K, int V>
+hipError_t launch_wy(const void* k, const void* v, const void* beta, const void* g, void* w, void* u,
+                     int64_t B, int64_t T, int64_t H, int sign, hipStream_t s) {
+  const int64_t NT = T / kBT;
+  const dim3 grid((unsigned)(B * NT * H));
+#define THM_WY_LAUNCH(SG)                                                                        \
+  hipLaunchKernelGGL((wy_fwd_kernel<K, V, SG>), grid, dim3(kWyThreads), 0, s, (const bf16*)k,    \
+                     (const bf16*)v, (const float*)beta, (const float*)g, (bf16*)w, (bf16*)u, T, H, NT)
+  if (sign < 0) THM_WY_LAUNCH(-1);
+  else THM_WY_LAUNCH(1);
+#undef THM_WY_LAUNCH
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace thm
+
+extern "C" int thm_wy_fwd(const void* k, const void* v, const void* beta, const void* g, void* w,
+                          void* u, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                          int32_t chunk_size, int32_t kv_dtype, int32_t sign, void* stream) {
+  using namespace thm;
+  if (chunk_size != kBT) return THM_ERR_BAD_ARGUMENT;
+  if (sign != 1 && sign != -1) return THM_ERR_BAD_ARGUMENT;
+  if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || T % kBT) return THM_ERR_BAD_SHAPE;
+  if (kv_dtype != THM_DTYPE_BF16) return THM_ERR_BAD_DTYPE;  // the fused path is bf16-only
+  if ((K != 64 && K != 128) || (V != 64 && V != 128)) return THM_ERR_UNSUPPORTED;
+  if (B == 0 || T == 0) return THM_OK;  // empty: nothing is read or written
+  if (!k || !v || !beta || !w || !u) return THM_ERR_NULL_POINTER;
+  if (((uintptr_t)k % 16) || ((uintptr_t)v % 16)) return THM_ERR_MISALIGNED;
+  if (((uintptr_t)w % 8) || ((uintptr_t)u % 8)) return THM_ERR_MISALIGNED;
+  if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
+  if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if (K == 64 && V == 64) e = launch_wy<64, 64>(k, v, beta, g, w, u, B, T, H, sign, s);
+  else if (K == 64 && V == 128) e = launch_wy<64, 128>(k, v, beta, g, w, u, B, T, H, sign, s);
+  else if (K == 128 && V == 64) e = launch_wy<128, 64>(k, v, beta, g, w, u, B, T, H, sign, s);
+  else e = launch_wy<128, 128>(k, v, beta, g, w, u, B, T, H, sign, s);
+  return (int)e;
+}

@@ -49,6 +49,7 @@ SIGNATURES = {
     "thm_wy_build_A": [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
                        _c_i32, _c_i32, _c_i32, _c_vp],
     "thm_chunk_local_cumsum": [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_vp],
+    "thm_wy_fwd": [_c_vp] * 6 + [_c_i64] * 5 + [_c_i32, _c_i32, _c_i32, _c_vp],
 }
 _RESTYPES = {"thm_status_string": ctypes.c_char_p}
 
