@@ -45,59 +45,88 @@ __device__ __forceinline__ void store_vec(XT* p, const float* v) {
   }
 }
 
-__device__ __forceinline__ float load_param(const void* p, int64_t i, int is_bf16) {
-  return is_bf16 ? (float)reinterpret_cast<const bf16*>(p)[i] : reinterpret_cast<const float*>(p)[i];
+template <typename WT>
+__device__ __forceinline__ float load_param(const void* p, int64_t i) {
+  return to_f32(reinterpret_cast<const WT*>(p)[i]);
 }
 
-template <typename XT, int VEC, int W, int NV>
+template <typename XT, typename WT, int VEC, int W, int NV>
 __global__ void __launch_bounds__(kConvWaves * kWave)
 causal_conv1d_kernel(const XT* __restrict__ x, const void* __restrict__ weight,
                      const void* __restrict__ bias, XT* __restrict__ out, int64_t n_rows,
-                     int64_t dim, int64_t seqlen, int64_t segs_per_row, int w_is_bf16, int act) {
+                     int64_t dim, int64_t seqlen, int64_t segs_per_row, int act) {
   constexpr int SEG = NV * kWave * VEC;
   constexpr int P = (W - 1 + VEC - 1) / VEC;  // previous vectors a lane needs
   constexpr int PA = P > 0 ? P : 1;
 
   const int lane = lane_id();
-  const int64_t seg = (int64_t)blockIdx.x * kConvWaves + (threadIdx.x / kWave);
+  // The wave index is uniform; saying so makes the row, its weights and the
+  // halo scalar (s_load) rather than per-lane loads behind divergent branches.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int64_t seg = (int64_t)blockIdx.x * kConvWaves + wave;
   if (seg >= n_rows * segs_per_row) return;  // wave-uniform exit
   const int64_t row = seg / segs_per_row;
   const int64_t s0 = (seg - row * segs_per_row) * SEG;
   const int64_t d = row % dim;
 
-  float wk[W];
-#pragma unroll
-  for (int k = 0; k < W; ++k) wk[k] = load_param(weight, d * W + k, w_is_bf16);
-  const float b0 = bias ? load_param(bias, d, w_is_bf16) : 0.f;
-
   const XT* __restrict__ xr = x + row * seqlen;
   XT* __restrict__ orow = out + row * seqlen;
 
-  // This lane's vectors.
-  float cur[NV][VEC];
+  float cur[NV][VEC];   // this lane's vectors
+  float halo[PA][VEC];  // vectors just left of the segment (stream index -1-q), wave-uniform
+  if constexpr (VEC * sizeof(XT) == 16) {
+    // Every load of the wave is issued before the first use: the segment's
+    // vectors (a lane past the row end reads the row start and is zeroed) and
+    // the P vectors left of the segment (uniform; none for the row's first
+    // segment, where they are the causal zero padding).
+    u32x4 raw[NV], hraw[PA];
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int64_t e0 = s0 + (int64_t)(j * kWave + lane) * VEC;
-    if (e0 < seqlen) {
-      load_vec<XT, VEC>(xr + e0, cur[j]);
-    } else {
+    for (int j = 0; j < NV; ++j) {
+      const int64_t e0 = s0 + (int64_t)(j * kWave + lane) * VEC;
+      raw[j] = ldg16_nt(xr + (e0 < seqlen ? e0 : 0));
+    }
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) cur[j][i] = 0.f;
+    for (int q = 0; q < PA; ++q) {
+      const int64_t pos = s0 - (int64_t)(q + 1) * VEC;
+      hraw[q] = (q < P && pos >= 0) ? ldg16(xr + pos) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t e0 = s0 + (int64_t)(j * kWave + lane) * VEC;
+      unpack16(raw[j], cur[j], XT{});
+      if (e0 >= seqlen) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) cur[j][i] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < PA; ++q) unpack16(hraw[q], halo[q], XT{});
+  } else {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t e0 = s0 + (int64_t)(j * kWave + lane) * VEC;
+      if (e0 < seqlen) {
+        load_vec<XT, VEC>(xr + e0, cur[j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) cur[j][i] = 0.f;
+      }
+    }
+    // Only the elements within W-1 of the segment start are read.
+#pragma unroll
+    for (int q = 0; q < PA; ++q) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t pos = s0 - (int64_t)(q + 1) * VEC + e;
+        const bool needed = (q < P) && ((q + 1) * VEC - e <= W - 1);
+        halo[q][e] = (needed && pos >= 0) ? to_f32(xr[pos]) : 0.f;
+      }
     }
   }
-
-  // Vectors just left of the segment (stream index -1-q), wave-uniform; only
-  // the elements within W-1 of the segment start are read.
-  float halo[PA][VEC];
+  float wk[W];
 #pragma unroll
-  for (int q = 0; q < PA; ++q) {
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const int64_t pos = s0 - (int64_t)(q + 1) * VEC + e;
-      const bool needed = (q < P) && ((q + 1) * VEC - e <= W - 1);
-      halo[q][e] = (needed && pos >= 0) ? to_f32(xr[pos]) : 0.f;
-    }
-  }
+  for (int k = 0; k < W; ++k) wk[k] = load_param<WT>(weight, d * W + k);
+  const float b0 = bias ? load_param<WT>(bias, d) : 0.f;
 
   // prev[p-1][j] = vector at stream index (j*64 + lane - p); only the elements
   // e >= p*VEC - (W-1) are used.
@@ -148,29 +177,27 @@ causal_conv1d_kernel(const XT* __restrict__ x, const void* __restrict__ weight,
   }
 }
 
-template <typename XT, int VEC, int W>
+template <typename XT, typename WT, int VEC, int W>
 hipError_t launch_conv(const void* x, const void* weight, const void* bias, void* out,
-                       int64_t n_rows, int64_t dim, int64_t seqlen, int w_is_bf16, int act,
-                       hipStream_t stream) {
+                       int64_t n_rows, int64_t dim, int64_t seqlen, int act, hipStream_t stream) {
   constexpr int SEG = kConvNV * kWave * VEC;
   const int64_t segs_per_row = (seqlen + SEG - 1) / SEG;
   const int64_t n_seg = n_rows * segs_per_row;
   const int64_t blocks = (n_seg + kConvWaves - 1) / kConvWaves;
-  hipLaunchKernelGGL((causal_conv1d_kernel<XT, VEC, W, kConvNV>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((causal_conv1d_kernel<XT, WT, VEC, W, kConvNV>), dim3((unsigned)blocks),
                      dim3(kConvWaves * kWave), 0, stream, (const XT*)x, weight, bias, (XT*)out,
-                     n_rows, dim, seqlen, segs_per_row, w_is_bf16, act);
+                     n_rows, dim, seqlen, segs_per_row, act);
   return hipGetLastError();
 }
 
-template <typename XT, int VEC>
-hipError_t dispatch_width(int width, const void* x, const void* weight, const void* bias,
-                          void* out, int64_t n_rows, int64_t dim, int64_t seqlen, int w_is_bf16,
-                          int act, hipStream_t s) {
+template <typename XT, int VEC, typename WT>
+hipError_t dispatch_width_w(int width, const void* x, const void* weight, const void* bias,
+                            void* out, int64_t n_rows, int64_t dim, int64_t seqlen, int act,
+                            hipStream_t s) {
   switch (width) {
 #define THM_CONV_W(WV)                                                                           \
   case WV:                                                                                       \
-    return launch_conv<XT, VEC, WV>(x, weight, bias, out, n_rows, dim, seqlen, w_is_bf16, act, \
-                                    s);
+    return launch_conv<XT, WT, VEC, WV>(x, weight, bias, out, n_rows, dim, seqlen, act, s);
     THM_CONV_W(1)
     THM_CONV_W(2)
     THM_CONV_W(3)
@@ -183,6 +210,14 @@ hipError_t dispatch_width(int width, const void* x, const void* weight, const vo
     default:
       return hipErrorInvalidValue;
   }
+}
+
+template <typename XT, int VEC>
+hipError_t dispatch_width(int width, const void* x, const void* weight, const void* bias,
+                          void* out, int64_t n_rows, int64_t dim, int64_t seqlen, int w_is_bf16,
+                          int act, hipStream_t s) {
+  return w_is_bf16 ? dispatch_width_w<XT, VEC, bf16>(width, x, weight, bias, out, n_rows, dim, seqlen, act, s)
+                   : dispatch_width_w<XT, VEC, float>(width, x, weight, bias, out, n_rows, dim, seqlen, act, s);
 }
 
 }  // namespace

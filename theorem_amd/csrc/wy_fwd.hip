@@ -96,7 +96,8 @@ wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
     const int j = q / C::kCPR;
     const int col = (q - j * C::kCPR) * 8;
     const int64_t row = (tok0 + j) * H + h;
-    xr[it] = ldg16(col < K ? (const void*)(k + row * K + col) : (const void*)(v + row * V + (col - K)));
+    // Non-temporal: read once here (measured 1% faster at config 4).
+    xr[it] = ldg16_nt(col < K ? (const void*)(k + row * K + col) : (const void*)(v + row * V + (col - K)));
   }
   lds_barrier();
 
