@@ -24,8 +24,15 @@ namespace {
 constexpr int kClThreads = 256;
 constexpr int kClSeg = 64;  // timesteps per lane
 
+constexpr int kClDepth = 16;  // time steps whose loads are in flight ahead of use
+
 __device__ __forceinline__ float conv_param(const void* p, int64_t i, int is_bf16) {
   return is_bf16 ? (float)reinterpret_cast<const bf16*>(p)[i] : reinterpret_cast<const float*>(p)[i];
+}
+
+template <typename WT>
+__device__ __forceinline__ float conv_param_t(const void* p, int64_t i) {
+  return to_f32(reinterpret_cast<const WT*>(p)[i]);
 }
 
 template <typename XT, int VEC>
@@ -48,12 +55,11 @@ __device__ __forceinline__ void cl_store(XT* p, const float* v) {
   }
 }
 
-template <typename XT, int VEC, int W>
+template <typename XT, typename WT, int VEC, int W, bool SILU>
 __global__ void __launch_bounds__(kClThreads)
 causal_conv1d_cl_kernel(const XT* __restrict__ x, const void* __restrict__ weight,
                         const void* __restrict__ bias, XT* __restrict__ out, int64_t seqlen,
-                        int64_t dim, int64_t groups, int64_t blocks_per_seg, int64_t segs,
-                        int w_is_bf16, int act) {
+                        int64_t dim, int64_t groups, int64_t blocks_per_seg, int64_t segs) {
   const int64_t blk = blockIdx.x;
   const int64_t cb = blk % blocks_per_seg;
   const int64_t bs = blk / blocks_per_seg;
@@ -64,38 +70,55 @@ causal_conv1d_cl_kernel(const XT* __restrict__ x, const void* __restrict__ weigh
   const int64_t t0 = seg * kClSeg;
   const int64_t tend = (t0 + kClSeg < seqlen) ? t0 + kClSeg : seqlen;
 
-  float wk[W][VEC], bv[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-#pragma unroll
-    for (int k = 0; k < W; ++k) wk[k][v] = conv_param(weight, (d0 + v) * W + k, w_is_bf16);
-    bv[v] = bias ? conv_param(bias, d0 + v, w_is_bf16) : 0.f;
-  }
-
   const XT* __restrict__ xb = x + b * seqlen * dim + d0;
   XT* __restrict__ ob = out + b * seqlen * dim + d0;
-  // win[k] = input at t - (W-1) + k for k < W-1 (zero before t = 0).
+  // A whole segment of 16-byte vectors runs as straight-line code with
+  // kClDepth loads in flight ahead of use (no loop, so the compiler's wait
+  // counts stay exact); a partial last segment, or scalar lanes, loop.
+  const bool pipelined = VEC * sizeof(XT) == 16 && tend - t0 == kClSeg;
+  u32x4 pf[kClDepth];
+  if constexpr (VEC * sizeof(XT) == 16) {
+    if (pipelined) {
+#pragma unroll
+      for (int i = 0; i < kClDepth; ++i) pf[i] = ldg16_nt(xb + (t0 + i) * dim);
+    }
+  }
+  // win[k] = input at t - (W-1) + k for k < W-1 (zero before t = 0): loaded
+  // from a clamped row, then zeroed, so every load is issued before any use.
   float win[W > 1 ? W - 1 : 1][VEC];
 #pragma unroll
   for (int k = 0; k < W - 1; ++k) {
     const int64_t t = t0 - (W - 1) + k;
-    if (t >= 0) {
-      cl_load<XT, VEC>(xb + t * dim, win[k]);
-    } else {
+    cl_load<XT, VEC>(xb + (t >= 0 ? t : 0) * dim, win[k]);
+    if (t < 0) {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) win[k][v] = 0.f;
     }
   }
-  for (int64_t t = t0; t < tend; ++t) {
-    float cur[VEC], res[VEC];
-    cl_load<XT, VEC>(xb + t * dim, cur);
+  // Weights and bias (bias absent: read the weights, then zero).
+  const WT* __restrict__ wp = reinterpret_cast<const WT*>(weight);
+  const WT* __restrict__ bp = bias ? reinterpret_cast<const WT*>(bias) : wp;
+  float wk[W][VEC], bv[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+#pragma unroll
+    for (int k = 0; k < W; ++k) wk[k][v] = to_f32(wp[(d0 + v) * W + k]);
+    bv[v] = to_f32(bp[d0 + v]);
+  }
+  if (!bias) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) bv[v] = 0.f;
+  }
+
+  auto step = [&](int64_t t, const float* cur) {
+    float res[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
       float acc = bv[v];
 #pragma unroll
       for (int k = 0; k < W - 1; ++k) acc = __builtin_fmaf(wk[k][v], win[k][v], acc);
       acc = __builtin_fmaf(wk[W - 1][v], cur[v], acc);
-      if (act == THM_ACT_SILU) acc = acc / (1.f + fast_exp(-acc));
+      if constexpr (SILU) acc = acc / (1.f + fast_exp(-acc));
       res[v] = acc;
     }
     cl_store<XT, VEC>(ob + t * dim, res);
@@ -107,12 +130,30 @@ causal_conv1d_cl_kernel(const XT* __restrict__ x, const void* __restrict__ weigh
 #pragma unroll
       for (int v = 0; v < VEC; ++v) win[W - 2][v] = cur[v];
     }
+  };
+
+  if constexpr (VEC * sizeof(XT) == 16) {
+    if (pipelined) {
+#pragma unroll
+      for (int i = 0; i < kClSeg; ++i) {
+        float cur[VEC];
+        unpack16(pf[i % kClDepth], cur, XT{});
+        if (i + kClDepth < kClSeg) pf[i % kClDepth] = ldg16_nt(xb + (t0 + i + kClDepth) * dim);
+        step(t0 + i, cur);
+      }
+      return;
+    }
+  }
+  for (int64_t t = t0; t < tend; ++t) {
+    float cur[VEC];
+    cl_load<XT, VEC>(xb + t * dim, cur);
+    step(t, cur);
   }
 }
 
-template <typename XT, int VEC>
-hipError_t launch_cl(int width, const void* x, const void* weight, const void* bias, void* out,
-                     int64_t batch, int64_t seqlen, int64_t dim, int wb, int act, hipStream_t s) {
+template <typename XT, typename WT, int VEC>
+hipError_t launch_cl_w(int width, const void* x, const void* weight, const void* bias, void* out,
+                       int64_t batch, int64_t seqlen, int64_t dim, int act, hipStream_t s) {
   const int64_t groups = dim / VEC;
   const int64_t blocks_per_seg = (groups + kClThreads - 1) / kClThreads;
   const int64_t segs = (seqlen + kClSeg - 1) / kClSeg;
@@ -120,9 +161,14 @@ hipError_t launch_cl(int width, const void* x, const void* weight, const void* b
   switch (width) {
 #define THM_CL_W(WV)                                                                          \
   case WV:                                                                                    \
-    hipLaunchKernelGGL((causal_conv1d_cl_kernel<XT, VEC, WV>), grid, dim3(kClThreads), 0, s, \
-                       (const XT*)x, weight, bias, (XT*)out, seqlen, dim, groups,             \
-                       blocks_per_seg, segs, wb, act);                                        \
+    if (act == THM_ACT_SILU)                                                                       \
+      hipLaunchKernelGGL((causal_conv1d_cl_kernel<XT, WT, VEC, WV, true>), grid, dim3(kClThreads), 0, \
+                         s, (const XT*)x, weight, bias, (XT*)out, seqlen, dim, groups,             \
+                         blocks_per_seg, segs);                                                    \
+    else                                                                                           \
+      hipLaunchKernelGGL((causal_conv1d_cl_kernel<XT, WT, VEC, WV, false>), grid, dim3(kClThreads), 0,\
+                         s, (const XT*)x, weight, bias, (XT*)out, seqlen, dim, groups,             \
+                         blocks_per_seg, segs);                                                    \
     break;
     THM_CL_W(1)
     THM_CL_W(2)
@@ -137,6 +183,13 @@ hipError_t launch_cl(int width, const void* x, const void* weight, const void* b
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <typename XT, int VEC>
+hipError_t launch_cl(int width, const void* x, const void* weight, const void* bias, void* out,
+                     int64_t batch, int64_t seqlen, int64_t dim, int wb, int act, hipStream_t s) {
+  return wb ? launch_cl_w<XT, bf16, VEC>(width, x, weight, bias, out, batch, seqlen, dim, act, s)
+            : launch_cl_w<XT, float, VEC>(width, x, weight, bias, out, batch, seqlen, dim, act, s);
 }
 
 template <typename XT>
