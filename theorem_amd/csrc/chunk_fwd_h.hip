@@ -346,8 +346,13 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
 //   P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}) on this wave's rows,
 //   one 16-row tile at a time; h[c] = S is stored tile by tile inside P2,
 //   before each tile's update (delta form) or after it (reference form).
-// h and v_new are written as 16- / 8-byte lane stores after a 4x4 quad
-// transpose of the accumulators.  Every DMA and store of the chunk loop is
+// h and v_new are written as 16- / 8-byte lane stores after the accumulators
+// are re-laid out so that each quad of lanes covers one contiguous piece of a
+// row (vmem.h acc_to_row_quads); only wave 0 loads the chunk's gates (a
+// strided 64-lane gather is the costliest DMA instruction per byte).  The
+// address unit of a CU, not HBM, bounded the earlier layout: at B = 1 (32
+// workgroups) a chunk took ~5800 cycles, of which ~4600 were address-unit
+// time for the chunk's DMA and stores.  Every DMA and store of the chunk loop is
 // issued through vmem.h, so the wait at the top of the loop is an exact count:
 // after this wave's DMA of chunk c it has issued NS - 1 chunks of stores and
 // NS - 2 chunks of DMA.
@@ -359,7 +364,7 @@ struct PCfg {
   static constexpr int kTileK = kBT * kRowK;            // bytes per k / w tile
   static constexpr int kRowU = kHBV * 2;                // bytes per u row of the V-tile
   static constexpr int kTileU = kBT * kRowU;
-  static constexpr int kGBytes = kWaves * kBT * 4;      // one gate copy per wave
+  static constexpr int kGBytes = 1024;                  // the chunk's 64 gates (wave 0's DMA), padded
   static constexpr int kStage = kTileK * (DELTA ? 2 : 1) + kTileU + (HAS_G ? kGBytes : 0);
   static constexpr int kXBytes = (DELTA && KS == 2) ? kWaves * 4 * 64 * 16 : 0;  // P1 partials
   static constexpr int kLds = NS * kStage + kXBytes;
@@ -368,16 +373,21 @@ struct PCfg {
   static constexpr int kKDma = kTileK / 1024 / kWaves;  // 1 KiB DMA instructions per wave per k tile
   static constexpr int kUDma = kTileU / 1024 / kWaves;
   static constexpr int kJbStore = 4 / KS;               // v_new row tiles stored per wave
-  static constexpr int kDma = kKDma * (DELTA ? 2 : 1) + kUDma + (HAS_G ? 1 : 0);
+  // DMA instructions per chunk: every wave's share of the k, w, u tiles, plus
+  // the gate load that only wave 0 issues.
+  static constexpr int kDma = kKDma * (DELTA ? 2 : 1) + kUDma;
+  static constexpr int kDma0 = kDma + (HAS_G ? 1 : 0);
   static constexpr int kStores = KBH + ((DELTA && STORE_VN) ? kJbStore : 0);
   static constexpr int kWaitFirst = (NS - 2) * kDma;
+  static constexpr int kWaitFirst0 = (NS - 2) * kDma0;
   static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma;
+  static constexpr int kWaitSteady0 = (NS - 1) * kStores + (NS - 2) * kDma0;
   static_assert(KS == 1 || KS == 2, "K split");
   static_assert(NS >= 2, "at least double buffering");
   static_assert(kKDma >= 1 && kUDma >= 1, "whole DMA instructions per wave");
   static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
   static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert(kWaitSteady <= 63, "vmcnt range");
+  static_assert(kWaitSteady0 <= 63, "vmcnt range");
 };
 
 template <int K, int V, int KS, int NS, bool DELTA, bool HAS_G, bool STORE_VN>
@@ -455,8 +465,12 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
 #pragma unroll
     for (int i = 0; i < C::kUDma; ++i) dma_b128(ub, uoff[i], __builtin_amdgcn_readfirstlane(lu + i * 1024));
     if constexpr (HAS_G) {
-      const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
-      dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s)) + wi * 256));
+      // One copy of the gates for the workgroup: a 64-lane gather at a
+      // 4 H-byte stride costs the address unit ~60 cycles per instruction.
+      if (wi == 0) {
+        const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
+        dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s))));
+      }
     }
   };
 
@@ -473,18 +487,18 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
   // make the compiler wait for every outstanding operation inside the loop.
   wait_vmcnt<0>();
 
-  // Store offsets after the quad transpose: lane (grp, 4 m4 + qq) holds row
-  // 4 grp + qq of a 16-row tile at columns 16 wq + 4 m4 .. + 3.
-  const int m4 = li >> 2, qq = li & 3;
-  const uint32_t hoff0 = (uint32_t)(((kap0 + 4 * grp + qq) * V + v0 + 16 * wq + 4 * m4) * 4);
-  const uint32_t vnoff0 = (uint32_t)((4 * grp + qq) * tsv + (v0 + 16 * wq + 4 * m4) * 2);
+  // Store offsets after acc_to_row_quads: lane (grp, 4 ra + cb) holds row
+  // 4 grp + ra of a 16-row tile at columns 16 wq + 4 cb .. + 3.
+  const int ra = li >> 2, cb = li & 3;
+  const uint32_t hoff0 = (uint32_t)(((kap0 + 4 * grp + ra) * V + v0 + 16 * wq + 4 * cb) * 4);
+  const uint32_t vnoff0 = (uint32_t)((4 * grp + ra) * tsv + (v0 + 16 * wq + 4 * cb) * 2);
   // One 16-row tile of h[c] (this wave's rows 16 kb .. 16 kb + 15).  The tiles
   // are stored one at a time inside P2, each next to the MFMAs that update
   // it, instead of as a burst after the chunk's DMA issue: 441 against 483 us
   // at config 4, the stores no longer queue ahead of the next chunk's loads.
   auto store_h_tile = [&](int64_t c, int kb) {
     float* hb = hout + ((b * NT + c) * H + hh) * (int64_t)(K * V);
-    st_b128(hb, hoff0 + (uint32_t)(kb * 16 * V * 4), __builtin_bit_cast(u32x4, quad_transpose(S[kb])));
+    st_b128(hb, hoff0 + (uint32_t)(kb * 16 * V * 4), __builtin_bit_cast(u32x4, acc_to_row_quads(S[kb])));
   };
 
   if (NT > 0) {
@@ -493,8 +507,13 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
   }
   for (int64_t c = 0; c < NT; ++c) {
     const int s = (int)(c % NS);
-    if (c < NS - 1) wait_vmcnt<C::kWaitFirst>();
-    else wait_vmcnt<C::kWaitSteady>();
+    if (wi == 0) {
+      if (c < NS - 1) wait_vmcnt<C::kWaitFirst0>();
+      else wait_vmcnt<C::kWaitSteady0>();
+    } else {
+      if (c < NS - 1) wait_vmcnt<C::kWaitFirst>();
+      else wait_vmcnt<C::kWaitSteady>();
+    }
     lds_barrier();  // A: chunk c is in LDS; every wave is done with chunk c - 1
     {
       const int64_t cn = c + NS - 1;
@@ -503,18 +522,63 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
 
     const char* tk = stage_k(s);
     const char* tu = stage_u(s);
-    // v (or u) rows j = 16 jb + 4 grp + r of column 16 wq + li.
-    f32x4 vn[4];
+    // Every LDS read of the chunk is issued here, before any of the work that
+    // uses it, so the reads' latencies overlap each other and the VALU work
+    // below (at one LDS round trip per MFMA pair the chunk body took ~2900
+    // cycles).  The compiler keeps this order: the sched_barrier stops it from
+    // sinking the reads next to their uses.
+    // u (or v) rows j = 16 jb + 4 grp + r of column 16 wq + li.
+    bf16x4 ur[4];
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) {
-      const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(
+    for (int jb = 0; jb < 4; ++jb)
+      ur[jb] = ds_read_tr16(reinterpret_cast<const bf16*>(
           tu + hl::tile_off(16 * jb + 4 * grp + (li >> 2), 16 * wq + 4 * (li & 3), C::kRowU)));
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
-    }
-
+    // w rows 16 jb + li, this wave's K elements, paired order (A operand of P1).
+    bf16x4 wa[DELTA ? 4 : 1][C::KBH / 2][2];
     if constexpr (DELTA) {
       const char* tw = stage_w(s);
+#pragma unroll
+      for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int s2 = 0; s2 < C::KBH / 2; ++s2) {
+          const int e0 = kap0 + 32 * s2 + 4 * grp;
+          wa[jb][s2][0] = *reinterpret_cast<const bf16x4*>(tw + hl::tile_off(16 * jb + li, e0, C::kRowK));
+          wa[jb][s2][1] = *reinterpret_cast<const bf16x4*>(tw + hl::tile_off(16 * jb + li, e0 + 16, C::kRowK));
+        }
+    }
+    // k^T fragments of this wave's state rows (A operand of P2), paired order.
+    bf16x4 ka[C::KBH][2][2];
+#pragma unroll
+    for (int kb = 0; kb < C::KBH; ++kb)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int col = kap0 + 16 * kb + 4 * (li & 3);
+        ka[kb][s2][0] = ds_read_tr16(reinterpret_cast<const bf16*>(
+            tk + hl::tile_off(32 * s2 + 4 * grp + (li >> 2), col, C::kRowK)));
+        ka[kb][s2][1] = ds_read_tr16(reinterpret_cast<const bf16*>(
+            tk + hl::tile_off(32 * s2 + 16 + 4 * grp + (li >> 2), col, C::kRowK)));
+      }
+    // Gates of this lane's rows j0 = 32 s2 + 4 grp + r and j0 + 16.
+    float gl = 0.f;
+    f32x4 gr[2][2];
+    if constexpr (HAS_G) {
+      const float* gs = stage_g(s);
+      gl = gs[kBT - 1];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        gr[s2][0] = *reinterpret_cast<const f32x4*>(gs + 32 * s2 + 4 * grp);
+        gr[s2][1] = *reinterpret_cast<const f32x4*>(gs + 32 * s2 + 16 + 4 * grp);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x4 vn[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vn[jb][r] = (float)ur[jb][r];
+
+    if constexpr (DELTA) {
       bf16x8 sb[C::KBH / 2];
 #pragma unroll
       for (int s2 = 0; s2 < C::KBH / 2; ++s2) {
@@ -522,22 +586,18 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
                             S[2 * s2 + 1][0], S[2 * s2 + 1][1], S[2 * s2 + 1][2], S[2 * s2 + 1][3]};
         sb[s2] = to_bf16x8(f);
       }
+      // P1: this wave's K half of w S for v_new rows 16 jb .. 16 jb + 15.
       f32x4 part[4];
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         f32x4 acc = zero4();
-        const int row = 16 * jb + li;
 #pragma unroll
-        for (int s2 = 0; s2 < C::KBH / 2; ++s2) {
-          const int e0 = kap0 + 32 * s2 + 4 * grp;
-          const bf16x4 a0 = *reinterpret_cast<const bf16x4*>(tw + hl::tile_off(row, e0, C::kRowK));
-          const bf16x4 a1 = *reinterpret_cast<const bf16x4*>(tw + hl::tile_off(row, e0 + 16, C::kRowK));
-          acc = mfma16x16x32(concat(a0, a1), sb[s2], acc);
-        }
+        for (int s2 = 0; s2 < C::KBH / 2; ++s2) acc = mfma16x16x32(concat(wa[jb][s2][0], wa[jb][s2][1]), sb[s2], acc);
         part[jb] = acc;
-        if constexpr (KS == 2) *reinterpret_cast<f32x4*>(xbuf + ((wi * 4 + jb) * 64 + lane) * 4) = acc;
       }
       if constexpr (KS == 2) {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) *reinterpret_cast<f32x4*>(xbuf + ((wi * 4 + jb) * 64 + lane) * 4) = part[jb];
         lds_barrier();  // B: both K halves' partials are in LDS
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
@@ -553,10 +613,7 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
 #pragma unroll
         for (int jj = 0; jj < C::kJbStore; ++jj) {
           const int jb = C::kJbStore * kh + jj;
-          const f32x4 t = quad_transpose(vn[jb]);
-          bf16x4 o;
-          o[0] = (bf16)t[0]; o[1] = (bf16)t[1]; o[2] = (bf16)t[2]; o[3] = (bf16)t[3];
-          st_b64(vb, vnoff0 + (uint32_t)(16 * jb * tsv), __builtin_bit_cast(u32x2, o));
+          st_b64(vb, vnoff0 + (uint32_t)(16 * jb * tsv), acc_to_row_quads_bf16(vn[jb]));
         }
       }
     }
@@ -565,17 +622,14 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
     bf16x8 vh[2];
     float decay = 1.f;
     if constexpr (HAS_G) {
-      const float* gs = stage_g(s) + wi * kBT;
-      const float gl = gs[kBT - 1];
       decay = fast_exp(gl);
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
         float f[8];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int j0 = 32 * s2 + 4 * grp + r;
-          f[r] = vn[2 * s2][r] * fast_exp(gl - gs[j0]);
-          f[4 + r] = vn[2 * s2 + 1][r] * fast_exp(gl - gs[j0 + 16]);
+          f[r] = vn[2 * s2][r] * fast_exp(gl - gr[s2][0][r]);
+          f[4 + r] = vn[2 * s2 + 1][r] * fast_exp(gl - gr[s2][1][r]);
         }
         vh[s2] = to_bf16x8(f);
       }
@@ -592,14 +646,7 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
       if constexpr (DELTA) store_h_tile(c, kb);  // state before chunk c
       if constexpr (HAS_G) S[kb] *= decay;
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const int col = kap0 + 16 * kb + 4 * (li & 3);
-        const bf16x4 a = ds_read_tr16(reinterpret_cast<const bf16*>(
-            tk + hl::tile_off(32 * s2 + 4 * grp + (li >> 2), col, C::kRowK)));
-        const bf16x4 bq = ds_read_tr16(reinterpret_cast<const bf16*>(
-            tk + hl::tile_off(32 * s2 + 16 + 4 * grp + (li >> 2), col, C::kRowK)));
-        S[kb] = mfma16x16x32(concat(a, bq), vh[s2], S[kb]);
-      }
+      for (int s2 = 0; s2 < 2; ++s2) S[kb] = mfma16x16x32(concat(ka[kb][s2][0], ka[kb][s2][1]), vh[s2], S[kb]);
       if constexpr (!DELTA) store_h_tile(c, kb);  // state after chunk c
     }
   }

@@ -117,4 +117,39 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 v) {
   return r;
 }
 
+// Re-layout of a 16x16 accumulator tile for row-contiguous stores.  In the
+// MFMA layout lane 4m + q of each 16-lane group holds column 4m + q, rows 0..3
+// (v[0..3]).  Afterwards lane 4a + b holds row a, columns 4b .. 4b + 3, so the
+// four lanes of a quad cover 16 contiguous elements of one row.  A vector
+// store whose consecutive lanes fall in different rows is split into more
+// memory requests: a 16-row store of 16-byte lanes occupies a CU's address
+// unit for ~62 cycles in the quad-transposed layout and ~18 in this one
+// (measured on MI355X).  A quad transpose (DPP), then the lane transpose
+// 4a + b <- 4b + a through ds_bpermute.
+__device__ __forceinline__ int row_quad_src_addr() {
+  const int l = lane_id();
+  return ((l & ~15) + 4 * (l & 3) + ((l >> 2) & 3)) * 4;
+}
+__device__ __forceinline__ f32x4 acc_to_row_quads(f32x4 v) {
+  const f32x4 t = quad_transpose(v);  // lane 4m + q: row q, columns 4m .. 4m + 3
+  const int src = row_quad_src_addr();
+  f32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(t[i])));
+  return r;
+}
+// The same for a tile stored as bf16: the four values of a lane are packed
+// first, so the lane transpose moves two dwords instead of four.
+__device__ __forceinline__ u32x2 acc_to_row_quads_bf16(f32x4 v) {
+  const f32x4 t = quad_transpose(v);
+  bf16x4 o;
+  o[0] = (bf16)t[0]; o[1] = (bf16)t[1]; o[2] = (bf16)t[2]; o[3] = (bf16)t[3];
+  const u32x2 pk = __builtin_bit_cast(u32x2, o);
+  const int src = row_quad_src_addr();
+  u32x2 r;
+  r[0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)pk[0]);
+  r[1] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)pk[1]);
+  return r;
+}
+
 }  // namespace thm
