@@ -13,7 +13,11 @@ algorithmic bytes per launch / its average duration vs 8 TB/s.  ``traffic``
 is read from profiles/traffic_cfg4.json when that summary of rocprofv3
 FETCH_SIZE / WRITE_SIZE runs exists, else null.  ``cpu_baseline`` times the
 CPU oracle on a bounded sample (one batch element of the same workload) and
-scales to a full step.  ``shapes`` gives each kernel's latency at configs 0-3,
+scales to a full step.  ``floors`` times memory-only kernels that move each
+step kernel's algorithmic bytes in its own tile pattern with no compute
+(theorem_amd/csrc/floors.hip): the fastest this box moves those bytes in that
+pattern, reported per kernel as ``floor_us`` and ``of_floor`` (floor / kernel
+time) beside the 8 TB/s roofline.  ``shapes`` gives each kernel's latency at configs 0-3,
 the shapes the reference publishes numbers for; ``extensions`` times the
 kernels beyond the four (WY matrix, gate cumsum, channels-last conv, conv
 decode step) at config-4 sizes.
@@ -193,6 +197,57 @@ def shape_latencies(torch, dev, warmup: int = 5, iters: int = 50, batched: int =
 
 
 # --------------------------------------------------------------------------- extensions
+
+def pattern_floors(torch, inp, conv_in, reps: int = 5):
+    """Memory-only floor of each step kernel's access pattern (libtheorem_floors.so,
+    csrc/floors.hip): the same algorithmic bytes moved in the same tile pattern
+    with no compute, min over ``reps`` launches (HIP events on the current stream).
+    The conv's floor is a streaming copy of x into a buffer of its size."""
+    import ctypes
+
+    from theorem_amd.build import FLOORS_LIB
+
+    if not FLOORS_LIB.exists():
+        return None
+    lib = ctypes.CDLL(str(FLOORS_LIB))
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    stream = vp(torch.cuda.current_stream().cuda_stream)
+    P = lambda t: vp(t.data_ptr())  # noqa: E731
+    q, k, v, beta, g, A = (inp[n] for n in ("q", "k", "v", "beta", "g", "A"))
+    B, T, H, K = k.shape
+    if K != 128 or v.shape[-1] != 128:
+        return None
+    x = conv_in[0]
+    xo = torch.empty_like(x)
+    w2, u2, vn2, o2 = (torch.empty_like(k) for _ in range(4))
+    h2 = torch.empty(B, T // 64, H, K, K, device=k.device, dtype=torch.float32)
+    N = B * T * H
+    runs = {
+        "causal_conv1d": (lambda: lib.thm_floor_copy(P(x), P(xo), i64(x.numel() * x.element_size()), stream),
+                          2 * x.numel() * x.element_size()),
+        "recompute_w_u": (lambda: lib.thm_floor_wu(P(k), P(v), P(A), P(beta), P(g), P(w2), P(u2), i64(B), i64(T),
+                                                   i64(H), stream), N * (4 * 256 + 8 + 256)),
+        "chunk_fwd_h": (lambda: lib.thm_floor_h(P(k), P(w2), P(u2), P(g), P(h2), P(vn2), i64(B), i64(T), i64(H),
+                                                stream), N * (4 * 256 + 4) + (N // 64) * 65536),
+        "chunk_fwd_o": (lambda: lib.thm_floor_o(P(q), P(k), P(v), P(h2), P(g), P(o2), i64(B), i64(T), i64(H),
+                                                stream), N * (4 * 256 + 4) + (N // 64) * 65536),
+    }
+    out = {}
+    for name, (fn, by) in runs.items():
+        if fn() != 0:
+            return None
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3)
+        out[name] = {"us": round(best, 2), "bytes": by, "GBps": round(by / best / 1e3, 1)}
+    return out
+
 
 def work_build_A(B, T, H, K, eb=2):
     N = B * T * H
@@ -387,6 +442,15 @@ def main() -> int:
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
                 "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic}
 
+    floors = None
+    if not args.small:
+        print("[bench] memory-only pattern floors", file=sys.stderr, flush=True)
+        floors = pattern_floors(torch, inp, conv_in)
+        if floors:
+            for n in names:
+                kernels[n]["floor_us"] = floors[n]["us"]
+                kernels[n]["of_floor"] = round(floors[n]["us"] / kernels[n]["us"], 3)
+
     shapes = None
     if not args.no_shapes:
         print("[bench] per-shape latencies (configs 0-3)", file=sys.stderr, flush=True)
@@ -410,7 +474,8 @@ def main() -> int:
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded torch CPU generator; BASELINE.json config-4 distributions)",
         "config": {"workload": workload, "parallelism": "single GPU"},
-        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu, "shapes": shapes, "extensions": ext,
+        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu, "floors": floors, "shapes": shapes,
+        "extensions": ext,
     }
     print(json.dumps(line))
     return 0

@@ -36,6 +36,22 @@ def test_library_exports_every_declared_symbol():
     assert set(declared_symbols()) <= set(_capi.SIGNATURES), "ctypes signatures missing"
 
 
+def test_floors_library_loads_and_rejects_bad_calls():
+    """The measurement library of bench.py (memory-only pattern floors) loads,
+    exports its four kernels and rejects bad shapes on the host."""
+    from theorem_amd.build import FLOORS_LIB
+
+    lib = ctypes.CDLL(str(FLOORS_LIB))
+    for name in ("thm_floor_copy", "thm_floor_wu", "thm_floor_h", "thm_floor_o"):
+        assert hasattr(lib, name), name
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    assert lib.thm_floor_copy(vp(FAKE), vp(FAKE), i64(17), None) == -1  # not a multiple of 16
+    assert lib.thm_floor_h(vp(FAKE), vp(FAKE), vp(FAKE), vp(FAKE), vp(FAKE), vp(FAKE),
+                           i64(1), i64(100), i64(2), None) == -1  # T % 64 != 0
+    assert lib.thm_floor_o(None, vp(FAKE), vp(FAKE), vp(FAKE), vp(FAKE), vp(FAKE),
+                           i64(1), i64(64), i64(2), None) == -1  # NULL input
+
+
 def test_abi_version_and_status_strings():
     lib = _capi.load_library()
     assert lib.thm_abi_version() == _capi.ABI_VERSION

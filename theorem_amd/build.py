@@ -4,6 +4,9 @@ Usage: python -m theorem_amd.build [-v]
 
 Objects go to theorem_amd/_build/, the shared library to
 theorem_amd/lib/libtheorem_mi355x.so (loaded by theorem_amd.kernels._capi).
+A second library, theorem_amd/lib/libtheorem_floors.so (csrc/floors.hip),
+holds the memory-only pattern kernels bench.py times as each kernel's floor;
+it is measurement tooling, not part of the C ABI.
 """
 from __future__ import annotations
 
@@ -33,6 +36,9 @@ SOURCES = [
     "wy_fwd.hip",
     "gates.hip",
 ]
+
+FLOORS_SRC = "floors.hip"
+FLOORS_LIB = LIB_DIR / "libtheorem_floors.so"
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -82,6 +88,9 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = LIB_DIR / (LIB_NAME + ".tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB_PATH)
+    ftmp = LIB_DIR / (FLOORS_LIB.name + ".tmp")
+    _run([HIPCC, *COMMON_FLAGS, "-shared", "-o", str(ftmp), str(CSRC / FLOORS_SRC)], verbose)
+    os.replace(ftmp, FLOORS_LIB)
     return LIB_PATH
 
 

@@ -58,7 +58,7 @@ struct FCfg {
   static constexpr int kTileK = kBT * kRowK;
   static constexpr int kRowU = kFBV * 2;          // bytes per u row of the V-tile
   static constexpr int kTileU = kBT * kRowU;
-  static constexpr int kGBytes = 4 * kBT * 4;     // one gate copy per state wave
+  static constexpr int kGBytes = 1024;            // the chunk's 64 gates, padded to 1 KiB
   static constexpr int kStage = 3 * kTileK + kTileU + (HAS_G ? kGBytes : 0);
   static constexpr int KB = K / 16;               // 16-row state tiles per column group
   static constexpr int kPBytes = kBT * kBT * 2;   // the chunk's scores P, bf16
@@ -162,8 +162,12 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 #pragma unroll
     for (int i = 0; i < C::kUDma; ++i) dma_b128(ub, uoff[i], __builtin_amdgcn_readfirstlane(lu + i * 1024));
     if constexpr (HAS_G) {
-      const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
-      dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s)) + wq * 256));
+      // One copy of the gates (state wave 0): a 64-lane gather at a 4 H-byte
+      // stride is the costliest DMA instruction per byte.
+      if (wq == 0) {
+        const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
+        dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s))));
+      }
     }
   };
 
@@ -231,7 +235,10 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   };
 
   // Row-tile stores after the quad transpose: lane (grp, 4 m4 + qq) holds row
-  // 4 grp + qq of a 16-row tile at columns 16 wq + 4 m4 .. + 3.
+  // 4 grp + qq of a 16-row tile at columns 16 wq + 4 m4 .. + 3.  (The
+  // row-contiguous layout of vmem.h acc_to_row_quads, which chunk_fwd_h's
+  // stores use, is slower here: 366 against 356 us at config 4; the lane
+  // transpose lengthens the output waves' path, which bounds this kernel.)
   const int m4 = li >> 2, qq = li & 3;
   const uint32_t rowoff0 = (uint32_t)((4 * grp + qq) * tsv + (v0 + 16 * wq + 4 * m4) * 2);
   auto store_rows = [&](bf16* base, int ib, f32x4 val) {
@@ -265,7 +272,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     lds_barrier();  // A: chunk c is in LDS; every wave is done with chunk c - 1
     const char* tk = stage_k(s);
     const char* tq = stage_q(s);
-    const float* gs = HAS_G ? stage_g(s) + wq * kBT : nullptr;
+    const float* gs = HAS_G ? stage_g(s) : nullptr;
 
     f32x4 vn[4];    // state waves: v_new rows j = 16 jb + 4 grp + r of column 16 wq + li
     bf16x8 vp[2];   // state waves: v_new as bf16 B-operand pairs

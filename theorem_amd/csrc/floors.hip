@@ -1,0 +1,185 @@
+// Memory-only floors of the hot-path kernels' access patterns (measurement
+// tooling for bench.py, built as a separate library, libtheorem_floors.so).
+//
+// Each kernel here moves exactly the algorithmic bytes of one hot-path kernel
+// with that kernel's tile pattern, and computes nothing: its time is the
+// fastest this box moves those bytes in that pattern.  bench.py reports each
+// hot-path kernel against it beside the 8 TB/s published peak, because the
+// achievable HBM rate on MI355X depends strongly on the read / write mix
+// (a read-only stream reaches ~7 TB/s, a write-only one ~5.8 TB/s, and a
+// few percent of writes mixed into a read stream cost far more than their
+// own bytes).
+//
+// Layouts are the hot path's, at K = V = 128, bf16 (the config-4 shapes):
+//   q, k, w, v, u, o, v_new, w/u outputs: [B, T, H, 128] bf16 (256 B per token-head)
+//   A: [B, T, H, 64] fp32 (256 B per token-head);  h: [B, T/64, H, 128, 128] fp32
+//   beta, g: [B, T, H] fp32
+// One 256-thread workgroup per (b, chunk of 64 tokens, head) tile, head
+// fastest, every load of the tile issued before the first store, as the
+// tile-parallel hot-path kernels do.  Outputs hold XOR mixes of the inputs.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRow = 256;      // bytes per token-head row of every [B, T, H, 128] bf16 tensor
+constexpr int kHTile = 65536;  // bytes of one fp32 128 x 128 state
+
+__device__ __forceinline__ u32x4 ld_nt(const char* p) { return __builtin_nontemporal_load((const u32x4*)p); }
+__device__ __forceinline__ u32x4 ld(const char* p) { return *(const u32x4*)p; }
+__device__ __forceinline__ void st(char* p, u32x4 v) { *(u32x4*)p = v; }
+
+struct Tile {
+  int64_t tile, hh, tok0;
+};
+__device__ __forceinline__ Tile tile_of(int64_t T, int64_t H) {
+  Tile t;
+  t.tile = blockIdx.x;
+  t.hh = t.tile % H;
+  const int64_t bc = t.tile / H, NT = T / 64;
+  t.tok0 = (bc / NT) * T + (bc % NT) * 64;
+  return t;
+}
+// Byte offset of 16-byte piece i (0..3) of this thread within a tile's 64 rows.
+__device__ __forceinline__ int64_t row_off(const Tile& t, int64_t H, int i) {
+  const int q = threadIdx.x + i * 256, j = q / 16, col = (q % 16) * 16;
+  return ((t.tok0 + j) * H + t.hh) * kRow + col;
+}
+
+// causal_conv1d: a streaming copy of the same bytes (x read once, out written once).
+__global__ void __launch_bounds__(256) floor_copy_kernel(const char* __restrict__ src, char* __restrict__ dst,
+                                                         int64_t n16) {
+  // Piece i of thread t: 16-byte index (block * 4 + i) * 256 + t, so every
+  // load and store instruction covers 4 KiB of contiguous memory.
+  const int64_t i0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+  u32x4 r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i0 + i * 256 < n16) r[i] = ld_nt(src + (i0 + i * 256) * 16);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i0 + i * 256 < n16) __builtin_nontemporal_store(r[i], (u32x4*)(dst + (i0 + i * 256) * 16));
+}
+
+// recompute_w_u: k, v, A rows, beta, g in; w, u rows out.
+__global__ void __launch_bounds__(256) floor_wu_kernel(const char* __restrict__ k, const char* __restrict__ v,
+                                                       const char* __restrict__ A, const float* __restrict__ beta,
+                                                       const float* __restrict__ g, char* __restrict__ w,
+                                                       char* __restrict__ u, int64_t T, int64_t H) {
+  const Tile t = tile_of(T, H);
+  u32x4 kr[4], vr[4], ar[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t off = row_off(t, H, i);
+    kr[i] = ld_nt(k + off);
+    vr[i] = ld_nt(v + off);
+    ar[i] = ld(A + off);
+  }
+  float s = 0.f;
+  if (threadIdx.x < 64) {
+    const int64_t r = (t.tok0 + threadIdx.x) * H + t.hh;
+    s = beta[r] + g[r];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t off = row_off(t, H, i);
+    u32x4 a = ar[i];
+    a[0] ^= __float_as_uint(s);
+    st(w + off, kr[i] ^ a);
+    st(u + off, vr[i] ^ a);
+  }
+}
+
+// chunk_fwd_h (delta form): k, w, u rows and g in; the 64 KB state of the
+// tile and the v_new rows out.
+__global__ void __launch_bounds__(256) floor_h_kernel(const char* __restrict__ k, const char* __restrict__ w,
+                                                      const char* __restrict__ u, const float* __restrict__ g,
+                                                      char* __restrict__ h, char* __restrict__ vn, int64_t T,
+                                                      int64_t H) {
+  const Tile t = tile_of(T, H);
+  u32x4 kr[4], wr[4], ur[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t off = row_off(t, H, i);
+    kr[i] = ld_nt(k + off);
+    wr[i] = ld_nt(w + off);
+    ur[i] = ld_nt(u + off);
+  }
+  u32x4 x = kr[0] ^ kr[1] ^ kr[2] ^ kr[3] ^ wr[0] ^ wr[1] ^ wr[2] ^ wr[3];
+  if (threadIdx.x < 64) x[0] ^= __float_as_uint(g[(t.tok0 + threadIdx.x) * H + t.hh]);
+  char* hb = h + t.tile * (int64_t)kHTile;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) st(hb + (threadIdx.x + i * 256) * 16, x ^ ur[i & 3]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) st(vn + row_off(t, H, i), ur[i] ^ x);
+}
+
+// chunk_fwd_o: q, k, v rows, the tile's 64 KB state and g in; o rows out.
+__global__ void __launch_bounds__(256) floor_o_kernel(const char* __restrict__ q, const char* __restrict__ k,
+                                                      const char* __restrict__ v, const char* __restrict__ h,
+                                                      const float* __restrict__ g, char* __restrict__ o,
+                                                      int64_t T, int64_t H) {
+  const Tile t = tile_of(T, H);
+  u32x4 hr[16], qr[4], kr[4], vr[4];
+  const char* hb = h + t.tile * (int64_t)kHTile;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) hr[i] = ld_nt(hb + (threadIdx.x + i * 256) * 16);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t off = row_off(t, H, i);
+    qr[i] = ld_nt(q + off);
+    kr[i] = ld_nt(k + off);
+    vr[i] = ld_nt(v + off);
+  }
+  u32x4 x = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x ^= hr[i];
+  if (threadIdx.x < 64) x[0] ^= __float_as_uint(g[(t.tok0 + threadIdx.x) * H + t.hh]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) st(o + row_off(t, H, i), qr[i] ^ kr[i] ^ vr[i] ^ x);
+}
+
+bool tile_shape_ok(int64_t B, int64_t T, int64_t H) {
+  return B > 0 && T > 0 && H > 0 && T % 64 == 0 && B * (T / 64) * H <= (INT64_C(1) << 31) - 1;
+}
+
+}  // namespace
+
+// All pointers are device pointers; 16-byte aligned for the row tensors and
+// states, 4-byte for beta and g.  Return 0, -1 for a bad shape or pointer, or
+// the positive hipError_t of the launch.
+extern "C" int thm_floor_copy(const void* src, void* dst, int64_t nbytes, void* stream) {
+  if (!src || !dst || nbytes <= 0 || nbytes % 16 || ((uintptr_t)src | (uintptr_t)dst) % 16) return -1;
+  const int64_t n16 = nbytes / 16, per_block = 256 * 4;
+  hipLaunchKernelGGL(floor_copy_kernel, dim3((unsigned)((n16 + per_block - 1) / per_block)), dim3(256), 0,
+                     (hipStream_t)stream, (const char*)src, (char*)dst, n16);
+  return (int)hipGetLastError();
+}
+
+extern "C" int thm_floor_wu(const void* k, const void* v, const void* A, const void* beta, const void* g,
+                            void* w, void* u, int64_t B, int64_t T, int64_t H, void* stream) {
+  if (!tile_shape_ok(B, T, H) || !k || !v || !A || !beta || !g || !w || !u) return -1;
+  hipLaunchKernelGGL(floor_wu_kernel, dim3((unsigned)(B * (T / 64) * H)), dim3(256), 0, (hipStream_t)stream,
+                     (const char*)k, (const char*)v, (const char*)A, (const float*)beta, (const float*)g,
+                     (char*)w, (char*)u, T, H);
+  return (int)hipGetLastError();
+}
+
+extern "C" int thm_floor_h(const void* k, const void* w, const void* u, const void* g, void* h, void* vn,
+                           int64_t B, int64_t T, int64_t H, void* stream) {
+  if (!tile_shape_ok(B, T, H) || !k || !w || !u || !g || !h || !vn) return -1;
+  hipLaunchKernelGGL(floor_h_kernel, dim3((unsigned)(B * (T / 64) * H)), dim3(256), 0, (hipStream_t)stream,
+                     (const char*)k, (const char*)w, (const char*)u, (const float*)g, (char*)h, (char*)vn, T, H);
+  return (int)hipGetLastError();
+}
+
+extern "C" int thm_floor_o(const void* q, const void* k, const void* v, const void* h, const void* g, void* o,
+                           int64_t B, int64_t T, int64_t H, void* stream) {
+  if (!tile_shape_ok(B, T, H) || !q || !k || !v || !h || !g || !o) return -1;
+  hipLaunchKernelGGL(floor_o_kernel, dim3((unsigned)(B * (T / 64) * H)), dim3(256), 0, (hipStream_t)stream,
+                     (const char*)q, (const char*)k, (const char*)v, (const char*)h, (const float*)g, (char*)o, T,
+                     H);
+  return (int)hipGetLastError();
+}
