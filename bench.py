@@ -231,6 +231,11 @@ def pattern_floors(torch, inp, conv_in, reps: int = 5):
                                                 stream), N * (4 * 256 + 4) + (N // 64) * 65536),
         "chunk_fwd_o": (lambda: lib.thm_floor_o(P(q), P(k), P(v), P(h2), P(g), P(o2), i64(B), i64(T), i64(H),
                                                 stream), N * (4 * 256 + 4) + (N // 64) * 65536),
+        # extension kernels: the fused WY forward and the fused h + o
+        "wy_fwd": (lambda: lib.thm_floor_wy(P(k), P(v), P(beta), P(g), P(w2), P(u2), i64(B), i64(T), i64(H), stream),
+                   N * (4 * 256 + 8)),
+        "chunk_gated_delta_fwd": (lambda: lib.thm_floor_ho(P(q), P(k), P(w2), P(u2), P(g), P(o2), i64(B), i64(T),
+                                                           i64(H), stream), N * (5 * 256 + 4)),
     }
     out = {}
     for name, (fn, by) in runs.items():
@@ -460,6 +465,10 @@ def main() -> int:
     if not args.no_ext and not args.small:
         print("[bench] extension kernels", file=sys.stderr, flush=True)
         ext = extension_timings(torch, inp, conv_in)
+        for n in ("wy_fwd", "chunk_gated_delta_fwd"):
+            if floors and n in floors and n in ext:
+                ext[n]["floor_us"] = floors[n]["us"]
+                ext[n]["of_floor"] = round(floors[n]["us"] / ext[n]["us"], 3)
 
     cpu = None
     if not args.no_cpu:

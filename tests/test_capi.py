@@ -38,11 +38,11 @@ def test_library_exports_every_declared_symbol():
 
 def test_floors_library_loads_and_rejects_bad_calls():
     """The measurement library of bench.py (memory-only pattern floors) loads,
-    exports its four kernels and rejects bad shapes on the host."""
+    exports its kernels and rejects bad shapes on the host."""
     from theorem_amd.build import FLOORS_LIB
 
     lib = ctypes.CDLL(str(FLOORS_LIB))
-    for name in ("thm_floor_copy", "thm_floor_wu", "thm_floor_h", "thm_floor_o"):
+    for name in ("thm_floor_copy", "thm_floor_wu", "thm_floor_h", "thm_floor_o", "thm_floor_wy", "thm_floor_ho"):
         assert hasattr(lib, name), name
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     assert lib.thm_floor_copy(vp(FAKE), vp(FAKE), i64(17), None) == -1  # not a multiple of 16

@@ -141,6 +141,55 @@ __global__ void __launch_bounds__(256) floor_o_kernel(const char* __restrict__ q
   for (int i = 0; i < 4; ++i) st(o + row_off(t, H, i), qr[i] ^ kr[i] ^ vr[i] ^ x);
 }
 
+// Fused WY forward (A-builder + recompute_w_u, A kept on chip): k, v rows,
+// beta, g in; w, u rows out.
+__global__ void __launch_bounds__(256) floor_wy_kernel(const char* __restrict__ k, const char* __restrict__ v,
+                                                       const float* __restrict__ beta, const float* __restrict__ g,
+                                                       char* __restrict__ w, char* __restrict__ u, int64_t T,
+                                                       int64_t H) {
+  const Tile t = tile_of(T, H);
+  u32x4 kr[4], vr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t off = row_off(t, H, i);
+    kr[i] = ld_nt(k + off);
+    vr[i] = ld_nt(v + off);
+  }
+  u32x4 x = {0, 0, 0, 0};
+  if (threadIdx.x < 64) {
+    const int64_t r = (t.tok0 + threadIdx.x) * H + t.hh;
+    x[0] = __float_as_uint(beta[r] + g[r]);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t off = row_off(t, H, i);
+    st(w + off, kr[i] ^ x);
+    st(u + off, vr[i] ^ x);
+  }
+}
+
+// Fused h + o (the per-chunk states stay on chip): q, k, w, u rows and g in;
+// o rows out.
+__global__ void __launch_bounds__(256) floor_ho_kernel(const char* __restrict__ q, const char* __restrict__ k,
+                                                       const char* __restrict__ w, const char* __restrict__ u,
+                                                       const float* __restrict__ g, char* __restrict__ o,
+                                                       int64_t T, int64_t H) {
+  const Tile t = tile_of(T, H);
+  u32x4 qr[4], kr[4], wr[4], ur[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t off = row_off(t, H, i);
+    qr[i] = ld_nt(q + off);
+    kr[i] = ld_nt(k + off);
+    wr[i] = ld_nt(w + off);
+    ur[i] = ld_nt(u + off);
+  }
+  u32x4 x = {0, 0, 0, 0};
+  if (threadIdx.x < 64) x[0] = __float_as_uint(g[(t.tok0 + threadIdx.x) * H + t.hh]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) st(o + row_off(t, H, i), qr[i] ^ kr[i] ^ wr[i] ^ ur[i] ^ x);
+}
+
 bool tile_shape_ok(int64_t B, int64_t T, int64_t H) {
   return B > 0 && T > 0 && H > 0 && T % 64 == 0 && B * (T / 64) * H <= (INT64_C(1) << 31) - 1;
 }
@@ -172,6 +221,23 @@ extern "C" int thm_floor_h(const void* k, const void* w, const void* u, const vo
   if (!tile_shape_ok(B, T, H) || !k || !w || !u || !g || !h || !vn) return -1;
   hipLaunchKernelGGL(floor_h_kernel, dim3((unsigned)(B * (T / 64) * H)), dim3(256), 0, (hipStream_t)stream,
                      (const char*)k, (const char*)w, (const char*)u, (const float*)g, (char*)h, (char*)vn, T, H);
+  return (int)hipGetLastError();
+}
+
+extern "C" int thm_floor_wy(const void* k, const void* v, const void* beta, const void* g, void* w, void* u,
+                            int64_t B, int64_t T, int64_t H, void* stream) {
+  if (!tile_shape_ok(B, T, H) || !k || !v || !beta || !g || !w || !u) return -1;
+  hipLaunchKernelGGL(floor_wy_kernel, dim3((unsigned)(B * (T / 64) * H)), dim3(256), 0, (hipStream_t)stream,
+                     (const char*)k, (const char*)v, (const float*)beta, (const float*)g, (char*)w, (char*)u, T, H);
+  return (int)hipGetLastError();
+}
+
+extern "C" int thm_floor_ho(const void* q, const void* k, const void* w, const void* u, const void* g, void* o,
+                            int64_t B, int64_t T, int64_t H, void* stream) {
+  if (!tile_shape_ok(B, T, H) || !q || !k || !w || !u || !g || !o) return -1;
+  hipLaunchKernelGGL(floor_ho_kernel, dim3((unsigned)(B * (T / 64) * H)), dim3(256), 0, (hipStream_t)stream,
+                     (const char*)q, (const char*)k, (const char*)w, (const char*)u, (const float*)g, (char*)o, T,
+                     H);
   return (int)hipGetLastError();
 }
 
