@@ -140,6 +140,7 @@ int thm_recompute_w_u_fwd(const void* k, const void* v, const void* beta, const 
  * `chunk_fwd_h_kernel` (kernel.py:61-138); reference form = reference.py:50-97.
  *   kv_dtype: dtype of k, w, vu, v_new (F32 or BF16). g, h0, h, ht are fp32.
  *   g may be NULL (no gate). K, V in {64, 128}; T % 64 == 0.
+ *   k, w, vu, h and v_new must be 16-byte aligned; g, h0 and ht 4-byte.
  */
 int thm_chunk_fwd_h(const void* k, const void* w, const void* vu, const void* g,
                     const void* h0, void* h, void* v_new, void* ht,

@@ -82,6 +82,25 @@ def test_conv_validation():
     assert conv(B=0) == 0 and conv(S=0) == 0
 
 
+def test_chunk_fwd_h_validation():
+    lib = _capi.load_library()
+
+    def h(**kw):
+        a = dict(k=FAKE, w=FAKE, u=FAKE, g=FAKE, h0=None, h=FAKE, vn=FAKE, ht=FAKE, B=1, T=64, H=2, K=64,
+                 V=64, bt=64, kd=1, flags=_capi.THM_H_DELTA)
+        a.update(kw)
+        return lib.thm_chunk_fwd_h(a["k"], a["w"], a["u"], a["g"], a["h0"], a["h"], a["vn"], a["ht"], a["B"],
+                                   a["T"], a["H"], a["K"], a["V"], a["bt"], a["kd"], a["flags"], None)
+
+    assert h(k=None) == -1 and h(h=None) == -1 and h(w=None) == -1
+    assert h(T=65) == -2 and h(kd=3) == -3 and h(K=96) == -4 and h(flags=4) == -6 and h(bt=32) == -6
+    # h and v_new are written as 16-byte lane vectors: both must be 16-byte aligned.
+    assert h(h=FAKE + 4) == -5 and h(vn=FAKE + 8) == -5 and h(k=FAKE + 8) == -5
+    assert h(g=FAKE + 2) == -5 and h(ht=FAKE + 2) == -5
+    assert h(flags=0, vn=FAKE) == -6  # v_new exists only in the delta form
+    assert h(B=0) == 0
+
+
 def test_python_wrapper_rejects_cpu_tensors():
     from theorem_amd.kernels.causal_conv1d import custom_kernel
     x = torch.zeros(1, 4, 8)

@@ -213,6 +213,9 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
       S[kb][r] = h0 ? *reinterpret_cast<const float*>(cptr(h0, st_base) + s_off + (16 * kb + r) * V * 4) : 0.f;
 
   // v_new rows j = 16 jb + 4 grp + r of this lane's column, relative to the chunk base.
+  // (h and v_new are stored one element per lane: 16 consecutive lanes cover
+  // 64 / 32 contiguous bytes of a row.  The row-quad re-layout of the DMA
+  // kernel below is slower here: 31.0 against 25.6 us at config 3.)
   const uint32_t vn_off = (uint32_t)(4 * grp * tok_stride_v + vcol * EB);
   auto store_state = [&](int64_t c) {
     char* hb = reinterpret_cast<char*>(hout) + ((b * NT + c) * H + hh) * (int64_t)(K * V) * 4;
@@ -753,13 +756,13 @@ extern "C" int thm_chunk_fwd_h(const void* k, const void* w, const void* vu, con
   if (T == 0 && !ht) return THM_OK;  // no chunks and no final state: nothing to write
   // With T == 0 only h0 (optional) is read and ht written.
   if (T > 0 && (!k || !vu || !h || (delta && !w))) return THM_ERR_NULL_POINTER;
-  const void* ptrs16[] = {k, vu, w};
+  // k, w, u/v are read and h, v_new written as 16-byte vectors per lane.
+  const void* ptrs16[] = {k, vu, w, h, v_new};
   for (const void* p : ptrs16)
     if (p && ((uintptr_t)p % 16)) return THM_ERR_MISALIGNED;
-  const void* ptrs4[] = {g, h0, h, v_new, ht};
+  const void* ptrs4[] = {g, h0, ht};
   for (const void* p : ptrs4)
     if (p && ((uintptr_t)p % 4)) return THM_ERR_MISALIGNED;
-  if (v_new && kv_dtype == THM_DTYPE_BF16 && ((uintptr_t)v_new % 2)) return THM_ERR_MISALIGNED;
   if (B > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
   // Per-lane offsets within one chunk's token block are 32-bit.
   if (64 * H * (K > V ? K : V) * (kv_dtype == THM_DTYPE_F32 ? 4 : 2) > (INT64_C(1) << 31))

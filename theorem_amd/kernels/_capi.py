@@ -106,7 +106,16 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+# torch's current-stream handle of a device.  The raw accessor returns the same
+# hipStream_t as torch.cuda.current_stream(device).cuda_stream without building
+# a Stream object (~0.1 against ~1.9 µs per call, which matters at the small
+# task.yml shapes where the host side of a call is most of its latency).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
