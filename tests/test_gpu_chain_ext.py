@@ -180,6 +180,33 @@ def test_wy_fwd_matches_two_kernels_and_oracle(dev, K, V, sign, gate):
     assert_close(u, eu, 1e-2, 1e-2, f"u vs oracle K={K} V={V} sign={sign} gate={gate}")
 
 
+# Grids of at least two tiles per persistent workgroup (2 per CU, 1024 tiles on
+# 256 CUs) run the software-pipelined WY kernel; these shapes force it at
+# every K, V (both signs, with and without the gate).
+@pytest.mark.parametrize("K,V", [(64, 64), (64, 128), (128, 64), (128, 128)])
+@pytest.mark.parametrize("sign,gate", [(1, "logsigmoid"), (-1, None)])
+def test_wy_fwd_pipelined_path(dev, K, V, sign, gate):
+    B, T, H = 2, 8192, 4
+    k, beta, g = _A_inputs(B, T, H, K, torch.bfloat16, gate, seed=43, dev=dev)
+    gen = torch.Generator().manual_seed(44)
+    v = torch.randn(B, T, H, V, generator=gen).to(torch.bfloat16).to(dev)
+    w, u = chain.wy_fwd(k, v, beta, g, sign=sign)
+    A = recompute_w_u.build_A(k, beta, g, sign=sign)
+    w2, u2 = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V))
+    torch.cuda.synchronize()
+    assert torch.equal(w, w2), f"w differs from the two-kernel path (K={K} V={V} sign={sign} gate={gate})"
+    assert torch.equal(u, u2), f"u differs from the two-kernel path (K={K} V={V} sign={sign} gate={gate})"
+    # The oracle on the first and last 64-token chunks of batch 0 (A is chunk-local).
+    for t0 in (0, T - 64):
+        sl = slice(t0, t0 + 64)
+        kk, bb, vv = np_(k[:1, sl]), np_(beta[:1, sl]), np_(v[:1, sl])
+        gk = np_(g[:1, sl]) if g is not None else np.zeros((1, 64, H))
+        eA = odn.build_A(kk, bb, gk, sign=sign)
+        ew, eu = odn.recompute_w_u_ref(kk, vv, bb, eA, gk)
+        assert_close(w[:1, sl], ew, 1e-2, 1e-2, f"w vs oracle K={K} V={V} t0={t0}")
+        assert_close(u[:1, sl], eu, 1e-2, 1e-2, f"u vs oracle K={K} V={V} t0={t0}")
+
+
 def test_wy_fwd_empty_and_errors(dev):
     e = torch.empty(1, 0, 2, 64, device=dev, dtype=torch.bfloat16)
     w, u = chain.wy_fwd(e, e, torch.empty(1, 0, 2, device=dev), None)

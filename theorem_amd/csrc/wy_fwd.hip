@@ -48,6 +48,59 @@ struct WyCfg {
   static_assert(kBT * kCPR % kWyThreads == 0, "staging must divide evenly");
 };
 
+// Scaled A operands of wave wv from the inverted blocks Xb: A'[t][j] for
+// t = 16 wv + li, j = 32 s + 8 grp + 0..7, in X's block (wv, jb = 2 s + grp / 2),
+// columns 8 (grp & 1) + 0..7: A diag(beta e^g) for w and A diag(beta) for u,
+// each split into bf16 hi + lo, as recompute_w_u does with A read from HBM.
+struct WyOperands {
+  bf16x8 awh[2], awl[2], auh[2], aul[2];
+};
+__device__ __forceinline__ WyOperands wy_operands(const float* Xb, const float* sb, const float* sg, int wv) {
+  const int lane = lane_id(), grp = lane >> 4, li = lane & 15;
+  WyOperands op;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int jb = 2 * s + (grp >> 1);
+    const float* X = Xb + blk(wv, jb < wv ? jb : wv) * kBlk + li * kBP + 8 * (grp & 1);
+    float fw[8], fu[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = 32 * s + 8 * grp + i;
+      const float a = (jb <= wv) ? X[i] : 0.f;
+      fu[i] = a * sb[j];
+      fw[i] = fu[i] * fast_exp(sg[j]);
+    }
+    split_bf16x8(fw, op.awh[s], op.awl[s]);
+    split_bf16x8(fu, op.auh[s], op.aul[s]);
+  }
+  return op;
+}
+
+// D[n][t] = sum_j X[j][n] A'[t][j] for this wave's 16 tokens, stored to w / u:
+// the [k | v] tile xs (row pitch `pitch` bf16) gives the X^T fragments by
+// ds_read_b64_tr_b16; each lane ends with features 16 nb + 4 grp .. + 3 of
+// token t = 16 wv + li, one 8-byte store.  The products are recompute_w_u's.
+template <int K, int V>
+__device__ __forceinline__ void wy_products(const bf16* xs, int pitch, const WyOperands& op, bf16* w, bf16* u,
+                                            int64_t trow) {
+  const int lane = lane_id(), grp = lane >> 4;
+#pragma unroll
+  for (int nb = 0; nb < (K + V) / 16; ++nb) {
+    const bool is_w = 16 * nb < K;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int r0 = tr_row_natural(32 * s, 0), r1 = tr_row_natural(32 * s, 1);
+      const bf16x8 xh = frag_tr(xs, pitch, r0, r1, 16 * nb);
+      acc = mfma16x16x32(xh, is_w ? op.awh[s] : op.auh[s], acc);
+      acc = mfma16x16x32(xh, is_w ? op.awl[s] : op.aul[s], acc);
+    }
+    const int n = 16 * nb + 4 * grp;
+    if (is_w) store4(w + trow * K + n, acc);
+    else store4(u + trow * V + (n - K), acc);
+  }
+}
+
 template <int K, int V, int SIGN>
 __global__ void __launch_bounds__(kWyThreads)
 wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
@@ -104,24 +157,8 @@ wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
   // 3. X = (I + L)^{-1}.
   wy::invert_L(Lb, Xb, Tb, wv);
 
-  // 4. Scaled A operands: A'[t][j], t = 16 wv + li, j = 32 s + 8 grp + 0..7,
-  //    in X's block (wv, jb = 2 s + grp / 2), columns 8 (grp & 1) + 0..7.
-  bf16x8 awh[2], awl[2], auh[2], aul[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int jb = 2 * s + (grp >> 1);
-    const float* X = Xb + blk(wv, jb < wv ? jb : wv) * kBlk + li * kBP + 8 * (grp & 1);
-    float fw[8], fu[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int j = 32 * s + 8 * grp + i;
-      const float a = (jb <= wv) ? X[i] : 0.f;
-      fu[i] = a * sb[j];
-      fw[i] = fu[i] * fast_exp(sg[j]);
-    }
-    split_bf16x8(fw, awh[s], awl[s]);
-    split_bf16x8(fu, auh[s], aul[s]);
-  }
+  // 4. Scaled A operands of this wave (read from X before the tile overwrites it).
+  const WyOperands op = wy_operands(Xb, sb, sg, wv);
 
   // 5. Stage the tile over the inversion's blocks.
   lds_barrier();  // every wave has read its A operands
@@ -134,22 +171,114 @@ wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
   }
   lds_barrier();
 
-  // 6. D[n][t] = sum_j X[j][n] A'[t][j]; lane holds features 16 nb + 4 grp .. + 3 of token t.
-  const int64_t trow = (tok0 + 16 * wv + li) * H + h;
+  // 6. Products and stores.
+  wy_products<K, V>(xs, C::kPitch, op, w, u, (tok0 + 16 * wv + li) * H + h);
+}
+
+// ---------------------------------------------------------------------------
+// Grids of at least two tiles per persistent workgroup: software-pipelined.
+//
+// With one tile per workgroup, every resident workgroup of a CU moves through
+// the same phases at about the same time: a burst of loads, then the latency
+// of form_L and the inversion (seven barriers) with no memory traffic, then
+// the stores.  Here 2 workgroups per CU walk the tiles t, t + G, t + 2G, ...
+// (G = the grid) and each issues the next tile's [k | v], beta and g loads into
+// registers before computing the current tile, so those loads are in flight
+// through the current tile's form_L, inversion and products.  The [k | v]
+// tile is staged in LDS once and form_L takes its k fragments from there (the
+// one-tile kernel loads them separately from global memory).  The tile and
+// the inversion blocks have separate LDS (59 KB per workgroup).  The
+// arithmetic is the one-tile kernel's (wy_blocks.h, wy_operands,
+// wy_products), so w and u are bit-identical to it.
+constexpr int kWyPipeWGsPerCU = 2;
+
+template <int K, int V, int SIGN>
+__global__ void __launch_bounds__(kWyThreads, 2)
+wy_fwd_pipe_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
+                   const float* __restrict__ beta, const float* __restrict__ g, bf16* __restrict__ w,
+                   bf16* __restrict__ u, int64_t T, int64_t H, int64_t NT, int64_t tiles) {
+  using C = WyCfg<K, V>;
+  constexpr int KS = C::KS;
+  __shared__ __attribute__((aligned(16))) bf16 xs[kBT * C::kPitch];  // [k | v] tile
+  __shared__ float Lb[10 * kBlk];  // L = sign M, lower blocks
+  __shared__ float Xb[10 * kBlk];  // X = A_c, lower blocks
+  __shared__ float Tb[3 * kBlk];   // per-level partial products
+  __shared__ float sb[kBT], sg[kBT];
+
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
+  const int lane = tid & 63;
+  const int grp = lane >> 4, li = lane & 15;
+
+  // Tile -> (b, c, head), head fastest.
+  auto tok_of = [&](int64_t tile, int64_t& h) {
+    h = tile % H;
+    const int64_t bc = tile / H;
+    return (bc / NT) * T + (bc % NT) * kBT;
+  };
+
+  // Prefetched registers of one tile (thread q: row q / kCPR, 16-byte chunk q % kCPR).
+  u32x4 xr[C::kLoads];
+  float br = 0.f, gr = 0.f;
+  auto prefetch = [&](int64_t tile) {
+    int64_t h;
+    const int64_t tok0 = tok_of(tile, h);
 #pragma unroll
-  for (int nb = 0; nb < C::kNB; ++nb) {
-    const bool is_w = 16 * nb < K;
-    f32x4 acc = zero4();
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int r0 = tr_row_natural(32 * s, 0), r1 = tr_row_natural(32 * s, 1);
-      const bf16x8 xh = frag_tr(xs, C::kPitch, r0, r1, 16 * nb);
-      acc = mfma16x16x32(xh, is_w ? awh[s] : auh[s], acc);
-      acc = mfma16x16x32(xh, is_w ? awl[s] : aul[s], acc);
+    for (int it = 0; it < C::kLoads; ++it) {
+      const int q = tid + it * kWyThreads;
+      const int j = q / C::kCPR;
+      const int col = (q - j * C::kCPR) * 8;
+      const int64_t row = (tok0 + j) * H + h;
+      xr[it] = ldg16_nt(col < K ? (const void*)(k + row * K + col) : (const void*)(v + row * V + (col - K)));
     }
-    const int n = 16 * nb + 4 * grp;
-    if (is_w) store4(w + trow * K + n, acc);
-    else store4(u + trow * V + (n - K), acc);
+    if (tid < kBT) {
+      const int64_t row = (tok0 + tid) * H + h;
+      br = beta[row];
+      gr = g ? g[row] : 0.f;
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int it = 0; it < C::kLoads; ++it) {
+      const int q = tid + it * kWyThreads;
+      const int j = q / C::kCPR;
+      const int col = (q - j * C::kCPR) * 8;
+      *reinterpret_cast<u32x4*>(xs + j * C::kPitch + col) = xr[it];
+    }
+    if (tid < kBT) {
+      sb[tid] = br;
+      sg[tid] = gr;
+    }
+  };
+
+  int64_t t = blockIdx.x;
+  if (t >= tiles) return;  // whole workgroup
+  prefetch(t);
+  stage();
+  lds_barrier();
+  for (;;) {
+    const int64_t tn = t + gridDim.x;
+    if (tn < tiles) prefetch(tn);  // in flight while tile t computes
+    int64_t h;
+    const int64_t tok0 = tok_of(t, h);
+
+    // k fragments from the staged tile: fh[tb][s] = k[16 tb + li][32 s + 8 grp .. + 7].
+    bf16x8 fh[4][KS], fl[4][1];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) fh[tb][s] = load8(xs + (16 * tb + li) * C::kPitch + 32 * s + 8 * grp);
+    wy::form_L<SIGN, KS, false>(fh, fl, sb, sg, Lb, wv);
+    lds_barrier();
+    wy::invert_L(Lb, Xb, Tb, wv);  // ends with a barrier
+    const WyOperands op = wy_operands(Xb, sb, sg, wv);
+    wy_products<K, V>(xs, C::kPitch, op, w, u, (tok0 + 16 * wv + li) * H + h);
+
+    if (tn >= tiles) break;
+    lds_barrier();  // every wave is done with tile t's LDS
+    stage();
+    lds_barrier();
+    t = tn;
   }
 }
 
@@ -157,7 +286,19 @@ template <int K, int V>
 hipError_t launch_wy(const void* k, const void* v, const void* beta, const void* g, void* w, void* u,
                      int64_t B, int64_t T, int64_t H, int sign, hipStream_t s) {
   const int64_t NT = T / kBT;
-  const dim3 grid((unsigned)(B * NT * H));
+  const int64_t tiles = B * NT * H;
+  const int64_t pgrid = (int64_t)device_cu_count() * kWyPipeWGsPerCU;
+  if (pgrid > 0 && tiles >= 2 * pgrid) {
+#define THM_WY_PIPE_LAUNCH(SG)                                                                        \
+  hipLaunchKernelGGL((wy_fwd_pipe_kernel<K, V, SG>), dim3((unsigned)pgrid), dim3(kWyThreads), 0, s,   \
+                     (const bf16*)k, (const bf16*)v, (const float*)beta, (const float*)g, (bf16*)w, \
+                     (bf16*)u, T, H, NT, tiles)
+    if (sign < 0) THM_WY_PIPE_LAUNCH(-1);
+    else THM_WY_PIPE_LAUNCH(1);
+#undef THM_WY_PIPE_LAUNCH
+    return hipGetLastError();
+  }
+  const dim3 grid((unsigned)tiles);
 #define THM_WY_LAUNCH(SG)                                                                        \
   hipLaunchKernelGGL((wy_fwd_kernel<K, V, SG>), grid, dim3(kWyThreads), 0, s, (const bf16*)k,    \
                      (const bf16*)v, (const float*)beta, (const float*)g, (bf16*)w, (bf16*)u, T, H, NT)
