@@ -60,6 +60,26 @@ def test_build_A_vs_oracle(dev, K, dtype, sign, gate):
     assert np.abs(res).max() < 1e-4 * max(1.0, scale)
 
 
+# bf16 grids of at least two tiles per persistent workgroup (3 per CU) run the
+# software-pipelined A-builder: it must equal the one-tile kernel bit for bit
+# (compared on a slice small enough to take the one-tile path) and the oracle.
+@pytest.mark.parametrize("K", [64, 128])
+@pytest.mark.parametrize("sign,gate", [(1, "logsigmoid"), (-1, "mild"), (1, None)])
+def test_build_A_pipelined_path(dev, K, sign, gate):
+    B, T, H = 2, 8192, 8
+    k, beta, g = _A_inputs(B, T, H, K, torch.bfloat16, gate, seed=7, dev=dev)
+    A = recompute_w_u.build_A(k, beta, g, sign=sign)
+    sl = slice(T - 192, T)
+    gs = None if g is None else g[1:, sl].contiguous()
+    A1 = recompute_w_u.build_A(k[1:, sl].contiguous(), beta[1:, sl].contiguous(), gs, sign=sign)
+    torch.cuda.synchronize()
+    assert torch.equal(A[1:, sl], A1), f"pipelined A differs from the one-tile kernel (K={K} sign={sign})"
+    kk = np_(k[:1, :128])
+    gk = np_(g[:1, :128]) if g is not None else np.zeros((1, 128, H))
+    eA = odn.build_A(kk, np_(beta[:1, :128]), gk, sign=sign)
+    assert_close(A[:1, :128], eA, 0, 1e-4 * np.abs(eA).max(), f"A K={K} sign={sign} gate={gate}")
+
+
 @pytest.mark.parametrize("B,T,H,K,V,seed", [(1, 64, 2, 64, 64, 4242), (2, 128, 4, 64, 64, 5236),
                                            (1, 256, 4, 64, 128, 1001)])
 def test_build_A_matches_reference_generator(dev, B, T, H, K, V, seed):

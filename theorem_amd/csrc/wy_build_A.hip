@@ -38,6 +38,25 @@ using wy::kBP;
 constexpr int kBT = wy::kBT;
 constexpr int kABThreads = 256;
 
+// A_c rows of the inverted blocks Xb: thread (r = q / 16, chunk j4 = q % 16)
+// writes A[r][4 j4 .. + 3]; 16-byte stores, 4 full 256-byte rows per
+// wavefront instruction.
+__device__ __forceinline__ void store_A(const float* Xb, float* out, int64_t H) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < kBT * 16 / kABThreads; ++it) {
+    const int q = tid + it * kABThreads;
+    const int r = q >> 4, j0 = (q & 15) * 4;
+    const int ib = r >> 4, jb = j0 >> 4;
+    f32x4 v = zero4();
+    if (jb <= ib) {
+      const float* X = Xb + blk(ib, jb) * kBlk + (r & 15) * kBP + (j0 & 15);
+      v[0] = X[0]; v[1] = X[1]; v[2] = X[2]; v[3] = X[3];
+    }
+    *reinterpret_cast<f32x4*>(out + (int64_t)r * H * kBT + j0) = v;
+  }
+}
+
 template <typename IT, int K, int SIGN>
 __global__ void __launch_bounds__(kABThreads)
 wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
@@ -90,19 +109,101 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
   lds_barrier();
   wy::invert_L(Lb, Xb, Tb, wv);
 
-  // 5. A_c rows: thread (r = q / 16, chunk j4 = q % 16) writes A[r][4 j4 .. + 3].
-  float* out = A + (tok0 * H + h) * kBT;
+  // 5. A_c rows.
+  store_A(Xb, A + (tok0 * H + h) * kBT, H);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 k on grids of at least two tiles per persistent workgroup:
+// software-pipelined, as the fused WY kernel (wy_fwd.hip).  Workgroups walk
+// the tiles t, t + G, ... and issue the next tile's k rows (16-byte row-major
+// loads), beta and g into registers before computing the current tile, so the
+// loads are in flight through form_L and the inversion; the k tile is staged
+// in LDS and the MFMA fragments are read from there.  The arithmetic is the
+// one-tile kernel's, so A is bit-identical.
+constexpr int kABPipeWGsPerCU = 3;
+
+template <int K, int SIGN>
+__global__ void __launch_bounds__(kABThreads, kABPipeWGsPerCU)
+wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ beta,
+                       const float* __restrict__ g, float* __restrict__ A, int64_t T, int64_t H,
+                       int64_t NT, int64_t tiles) {
+  constexpr int KS = K / 32;
+  constexpr int kPitch = K + 8;                       // bf16 elements (16-byte pad)
+  constexpr int kCPR = K / 8;                         // 16-byte chunks per k row
+  constexpr int kLoads = kBT * kCPR / kABThreads;     // per thread
+  static_assert(kBT * kCPR % kABThreads == 0, "staging split");
+  __shared__ __attribute__((aligned(16))) bf16 ks[kBT * kPitch];
+  __shared__ float Lb[10 * kBlk];
+  __shared__ float Xb[10 * kBlk];
+  __shared__ float Tb[3 * kBlk];
+  __shared__ float sb[kBT], sg[kBT];
+
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6;
+  const int lane = tid & 63;
+  const int grp = lane >> 4, li = lane & 15;
+
+  auto tok_of = [&](int64_t tile, int64_t& h) {
+    h = tile % H;
+    const int64_t bc = tile / H;
+    return (bc / NT) * T + (bc % NT) * kBT;
+  };
+  u32x4 kr[kLoads];
+  float br = 0.f, gr = 0.f;
+  auto prefetch = [&](int64_t tile) {
+    int64_t h;
+    const int64_t tok0 = tok_of(tile, h);
 #pragma unroll
-  for (int it = 0; it < kBT * 16 / kABThreads; ++it) {
-    const int q = tid + it * kABThreads;
-    const int r = q >> 4, j0 = (q & 15) * 4;
-    const int ib = r >> 4, jb = j0 >> 4;
-    f32x4 v = zero4();
-    if (jb <= ib) {
-      const float* X = Xb + blk(ib, jb) * kBlk + (r & 15) * kBP + (j0 & 15);
-      v[0] = X[0]; v[1] = X[1]; v[2] = X[2]; v[3] = X[3];
+    for (int it = 0; it < kLoads; ++it) {
+      const int q = tid + it * kABThreads;
+      const int j = q / kCPR, col = (q - j * kCPR) * 8;
+      kr[it] = ldg16_nt(k + ((tok0 + j) * H + h) * K + col);
     }
-    *reinterpret_cast<f32x4*>(out + (int64_t)r * H * kBT + j0) = v;
+    if (tid < kBT) {
+      const int64_t row = (tok0 + tid) * H + h;
+      br = beta[row];
+      gr = g ? g[row] : 0.f;
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int it = 0; it < kLoads; ++it) {
+      const int q = tid + it * kABThreads;
+      const int j = q / kCPR, col = (q - j * kCPR) * 8;
+      *reinterpret_cast<u32x4*>(ks + j * kPitch + col) = kr[it];
+    }
+    if (tid < kBT) {
+      sb[tid] = br;
+      sg[tid] = gr;
+    }
+  };
+
+  int64_t t = blockIdx.x;
+  if (t >= tiles) return;  // whole workgroup
+  prefetch(t);
+  stage();
+  lds_barrier();
+  for (;;) {
+    const int64_t tn = t + gridDim.x;
+    if (tn < tiles) prefetch(tn);  // in flight while tile t computes
+    int64_t h;
+    const int64_t tok0 = tok_of(t, h);
+    bf16x8 fh[4][KS], fl[4][1];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) fh[tb][s] = load8(ks + (16 * tb + li) * kPitch + 32 * s + 8 * grp);
+    wy::form_L<SIGN, KS, false>(fh, fl, sb, sg, Lb, wv);
+    lds_barrier();
+    wy::invert_L(Lb, Xb, Tb, wv);  // ends with a barrier
+    store_A(Xb, A + (tok0 * H + h) * kBT, H);
+
+    if (tn >= tiles) break;
+    lds_barrier();  // every wave is done with tile t's LDS
+    stage();
+    lds_barrier();
+    t = tn;
   }
 }
 
@@ -110,7 +211,20 @@ template <typename IT, int K>
 hipError_t launch_A(const void* k, const void* beta, const void* g, void* A, int64_t B, int64_t T,
                     int64_t H, int sign, hipStream_t s) {
   const int64_t NT = T / kBT;
-  const dim3 grid((unsigned)(B * NT * H));
+  const int64_t tiles = B * NT * H;
+  if constexpr (std::is_same<IT, bf16>::value) {
+    const int64_t pgrid = (int64_t)device_cu_count() * kABPipeWGsPerCU;
+    if (pgrid > 0 && tiles >= 2 * pgrid) {
+      if (sign < 0)
+        hipLaunchKernelGGL((wy_build_A_pipe_kernel<K, -1>), dim3((unsigned)pgrid), dim3(kABThreads), 0, s,
+                           (const bf16*)k, (const float*)beta, (const float*)g, (float*)A, T, H, NT, tiles);
+      else
+        hipLaunchKernelGGL((wy_build_A_pipe_kernel<K, 1>), dim3((unsigned)pgrid), dim3(kABThreads), 0, s,
+                           (const bf16*)k, (const float*)beta, (const float*)g, (float*)A, T, H, NT, tiles);
+      return hipGetLastError();
+    }
+  }
+  const dim3 grid((unsigned)tiles);
   if (sign < 0)
     hipLaunchKernelGGL((wy_build_A_kernel<IT, K, -1>), grid, dim3(kABThreads), 0, s, (const IT*)k,
                        (const float*)beta, (const float*)g, (float*)A, T, H, NT);
