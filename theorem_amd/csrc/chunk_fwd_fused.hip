@@ -145,6 +145,29 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   }
   const uint32_t goff = (uint32_t)(lane * H * 4);
 
+  // Part m of the DMA of chunk cc into stage s: m = 0, 1, 2 the k, w, q tile,
+  // m = 3 the u tile and the gates.
+  auto issue_part = [&](int64_t cc, int s, int m) {
+    const int64_t off = kc0 + cc * kcs;
+    if (m < 3) {
+      const char* src = reinterpret_cast<const char*>(m == 0 ? k : m == 1 ? w : q) + off;
+      char* dst = m == 0 ? stage_k(s) : m == 1 ? stage_w(s) : stage_q(s);
+      const uint32_t l0 = lds_address(dst) + wq * C::kKDma * 1024;
+#pragma unroll
+      for (int i = 0; i < C::kKDma; ++i) dma_b128(src, koff[i], __builtin_amdgcn_readfirstlane(l0 + i * 1024));
+    } else {
+      const char* ub = reinterpret_cast<const char*>(u) + uc0 + cc * ucs;
+      const uint32_t lu = lds_address(stage_u(s)) + wq * C::kUDma * 1024;
+#pragma unroll
+      for (int i = 0; i < C::kUDma; ++i) dma_b128(ub, uoff[i], __builtin_amdgcn_readfirstlane(lu + i * 1024));
+      if constexpr (HAS_G) {
+        if (wq == 0) {
+          const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
+          dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s))));
+        }
+      }
+    }
+  };
   // DMA of chunk cc into stage s; issued by the state waves only.
   auto issue = [&](int64_t cc, int s) {
     const int64_t off = kc0 + cc * kcs;
@@ -277,11 +300,11 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     f32x4 vn[4];    // state waves: v_new rows j = 16 jb + 4 grp + r of column 16 wq + li
     bf16x8 vp[2];   // state waves: v_new as bf16 B-operand pairs
     if (state_wave) {
-      {
-        const int64_t cn = c + kFStages - 1;
-        issue(cn < NT ? cn : NT - 1, (int)(cn % kFStages));
-        prefetch(cn + 1 < NT ? cn + 1 : NT - 1);
-      }
+      // The next chunk's DMA is issued in four parts between P1's row blocks,
+      // so the address unit drains between parts while the MFMAs run.
+      const int64_t cn = c + kFStages - 1;
+      const int64_t cnc = cn < NT ? cn : NT - 1;
+      const int cns = (int)(cn % kFStages);
       // S as the B operand (pairs of 16-row tiles), also handed to the output wave.
       bf16x8 sb[KB2];
 #pragma unroll
@@ -296,12 +319,14 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       const char* tu = stage_u(s);
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
+        issue_part(cnc, cns, jb);
         const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(
             tu + hl::tile_off(16 * jb + 4 * grp + (li >> 2), 16 * wq + 4 * (li & 3), C::kRowU)));
 #pragma unroll
         for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
         vn[jb] -= rows_times_S(tw, jb, sb);
       }
+      prefetch(cn + 1 < NT ? cn + 1 : NT - 1);
       if constexpr (STORE_VN) {
         bf16* vb = vnew + ((b * T + c * kBT) * H + hh) * V;
 #pragma unroll
