@@ -146,4 +146,5 @@ def test_build_A_and_cumsum_validation():
     assert cs(T=100) == -2 and cs(H=0) == -2
     assert cs(ad=3) == -3 and cs(mode=2) == -6 and cs(bt=128) == -6
     assert cs(g=FAKE + 2) == -5 and cs(a=FAKE + 1, ad=1) == -5
+    assert cs(B=1 << 30, T=4096, H=64) == -2  # more (b, chunk, head) lanes than the grid can hold
     assert cs(B=0) == 0

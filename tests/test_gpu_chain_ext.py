@@ -200,13 +200,14 @@ def test_wy_fwd_matches_two_kernels_and_oracle(dev, K, V, sign, gate):
     assert_close(u, eu, 1e-2, 1e-2, f"u vs oracle K={K} V={V} sign={sign} gate={gate}")
 
 
-# Grids of at least two tiles per persistent workgroup (2 per CU, 1024 tiles on
+# Grids of at least two tiles per persistent workgroup (2 per CU: 1024 tiles on
 # 256 CUs) run the software-pipelined WY kernel; these shapes force it at
-# every K, V (both signs, with and without the gate).
+# every K, V (both signs, with and without the gate).  1280 tiles: the
+# workgroups get 2 or 3 tiles each.
 @pytest.mark.parametrize("K,V", [(64, 64), (64, 128), (128, 64), (128, 128)])
 @pytest.mark.parametrize("sign,gate", [(1, "logsigmoid"), (-1, None)])
 def test_wy_fwd_pipelined_path(dev, K, V, sign, gate):
-    B, T, H = 2, 8192, 4
+    B, T, H = 2, 8192, 5
     k, beta, g = _A_inputs(B, T, H, K, torch.bfloat16, gate, seed=43, dev=dev)
     gen = torch.Generator().manual_seed(44)
     v = torch.randn(B, T, H, V, generator=gen).to(torch.bfloat16).to(dev)
