@@ -269,6 +269,37 @@ def test_h_dma_pipeline_forms(dev, K, V, form):
         assert_close(ht, eht, 1e-2, 1e-2, f"final {form} K={K} V={V} T={T}")
 
 
+# fp32 grids of at least 256 workgroups run the register kernel with its
+# two-chunks-ahead prefetch (two register sets); T = 64 * (1, 2, 3, 4) covers
+# the odd / even chunk counts of its two-chunk loop.
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("form", ["delta", "reference_plain"])
+def test_h_fp32_deep_prefetch(dev, K, V, form):
+    B, H = 4, (64 if V == 64 else 32)
+    assert B * H * (V // 64) >= 256
+    for T in (64, 128, 192, 256):
+        d = configs.make_h_inputs(B, T, H, K, V, seed=13, device=dev, dtype=torch.float32, h0_std=0.1)
+        plain = form.endswith("plain")
+        g = None if plain else d["g"]
+        h0 = None if plain else d["h0"]
+        gk = np_(g) if g is not None else None
+        h0k = np_(h0) if h0 is not None else None
+        if form == "delta":
+            h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=g, initial_state=h0,
+                                                       output_final_state=True))
+            sync()
+            eh, evn, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np_(d["w"]), np_(d["u"]), gk, h0=h0k)
+            assert_close(vn, evn, 1e-3, 1e-3, f"v_new fp32 K={K} V={V} T={T}")
+        else:
+            h, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], v=d["u"], g=g, initial_state=h0,
+                                                   output_final_state=True))
+            sync()
+            pre, _, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np.zeros_like(np_(d["w"])), np_(d["u"]), gk, h0=h0k)
+            eh = np.concatenate([pre[:, 1:], eht[:, None]], axis=1)
+        assert_close(h, eh, 1e-3, 1e-3, f"h fp32 {form} K={K} V={V} T={T}")
+        assert_close(ht, eht, 1e-3, 1e-3, f"final fp32 {form} K={K} V={V} T={T}")
+
+
 def test_h_dma_pipeline_unaligned_head_count_and_empty(dev):
     # B * H not a multiple of 8 (the plain block mapping) and T = 0 on the DMA path.
     B, T, H, K, V = 1, 128, 260, 64, 64

@@ -91,7 +91,8 @@ __device__ __forceinline__ const char* cptr(const void* p, int64_t byte_off) {
   return reinterpret_cast<const char*>(p) + byte_off;
 }
 
-template <typename IT, int K, int V, bool DELTA, bool HAS_G>
+// DEEP: two register sets, two chunks ahead (see the chunk loop below).
+template <typename IT, int K, int V, bool DELTA, bool HAS_G, bool DEEP>
 __global__ void __launch_bounds__(kHThreads)
 chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT* __restrict__ vu,
                    const float* __restrict__ g, const float* __restrict__ h0,
@@ -226,15 +227,26 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
         *reinterpret_cast<float*>(hb + s_off + (16 * kb + r) * V * 4) = S[kb][r];
   };
 
-  Pf pf;
+  // With DEEP, two register sets run two chunks ahead: at chunk c `cur`
+  // holds chunk c + 1 (its loads issued during chunk c - 1) and `nxt`
+  // receives chunk c + 2, so the commit at the end of chunk c waits for loads
+  // a whole chunk old.  Without it one set is loaded at the top of chunk c
+  // and committed at its end.  DEEP is faster on large grids (fp32 at config
+  // 4: 890 -> 779 us) and slower on small ones (fp32 config 3: 38.9 -> 46.7
+  // us), where the chunk's own latency chain, not the loads, sets the period.
+  Pf pa, pb;
   if (NT > 0) {
-    prefetch(pf, 0);
-    commit(pf, stage(0));
+    prefetch(pa, 0);
+    commit(pa, stage(0));
+    if (DEEP && NT > 1) prefetch(pa, 1);
     lds_barrier();
   }
-  for (int64_t c = 0; c < NT; ++c) {
+  auto chunk = [&](int64_t c, Pf& cur, Pf& nxt) {
     const St cs = stage((int)(c % C::kStages));
-    if (c + 1 < NT) prefetch(pf, c + 1);
+    {
+      const int64_t pc = DEEP ? c + 2 : c + 1;
+      if (pc < NT) prefetch(nxt, pc);
+    }
     if constexpr (DELTA) store_state(c);  // state before chunk c
 
     // v_new (or v) for rows j = 16 jb + 4 grp + r of this lane's column.
@@ -307,7 +319,7 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
 
     if (c + 1 < NT) {
       if constexpr (C::kStages == 1) lds_barrier();  // every wave is done with the stage
-      commit(pf, stage((int)((c + 1) % C::kStages)));
+      commit(cur, stage((int)((c + 1) % C::kStages)));
     }
     lds_barrier();
     // v_new after the commit: stores queued behind the prefetch would make its
@@ -322,6 +334,14 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
             *reinterpret_cast<IT*>(vb + vn_off + (16 * jb + r) * tok_stride_v) = from_f32<IT>(vn[jb][r]);
       }
     }
+  };
+  if constexpr (DEEP) {
+    for (int64_t c = 0; c < NT; c += 2) {
+      chunk(c, pa, pb);
+      if (c + 1 < NT) chunk(c + 1, pb, pa);
+    }
+  } else {
+    for (int64_t c = 0; c < NT; ++c) chunk(c, pa, pa);
   }
 
   if (ht) {
@@ -705,15 +725,19 @@ hipError_t launch_h(const void* k, const void* w, const void* vu, const void* g,
   const int64_t NT = T / kBT;
   const int64_t BH = B * H;
   const dim3 grid((unsigned)(BH * (V / kHBV)));
+  const bool deep = BH * (V / kHBV) >= kHDmaMinGrid;  // bandwidth-bound regime
+#define THM_H_LAUNCH(HG, DP)                                                                      \
+  hipLaunchKernelGGL((chunk_fwd_h_kernel<IT, K, V, DELTA, HG, DP>), grid, dim3(kHThreads), 0, s,  \
+                     (const IT*)k, (const IT*)w, (const IT*)vu, (const float*)g, (const float*)h0, \
+                     (float*)h, (IT*)vnew, (float*)ht, T, H, NT, BH)
   if (g) {
-    hipLaunchKernelGGL((chunk_fwd_h_kernel<IT, K, V, DELTA, true>), grid, dim3(kHThreads), 0, s,
-                       (const IT*)k, (const IT*)w, (const IT*)vu, (const float*)g, (const float*)h0,
-                       (float*)h, (IT*)vnew, (float*)ht, T, H, NT, BH);
+    if (deep) THM_H_LAUNCH(true, true);
+    else THM_H_LAUNCH(true, false);
   } else {
-    hipLaunchKernelGGL((chunk_fwd_h_kernel<IT, K, V, DELTA, false>), grid, dim3(kHThreads), 0, s,
-                       (const IT*)k, (const IT*)w, (const IT*)vu, (const float*)g, (const float*)h0,
-                       (float*)h, (IT*)vnew, (float*)ht, T, H, NT, BH);
+    if (deep) THM_H_LAUNCH(false, true);
+    else THM_H_LAUNCH(false, false);
   }
+#undef THM_H_LAUNCH
   return hipGetLastError();
 }
 
