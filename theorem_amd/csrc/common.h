@@ -88,15 +88,9 @@ __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
 
-// Split an fp32 value into bf16 hi + lo with hi + lo == v to ~2^-16 relative.
-__device__ __forceinline__ void split_bf16(float v, bf16& hi, bf16& lo) {
-  hi = (bf16)v;
-  lo = (bf16)(v - (float)hi);
-}
 
-// 16-byte global load / store of raw bits.
+// 16-byte global load of raw bits; non-temporal (streaming) 16-byte load / store.
 __device__ __forceinline__ u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ void stg16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ u32x4 ldg16_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
@@ -104,11 +98,6 @@ __device__ __forceinline__ void stg16_nt(void* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
-// Non-temporal (streaming) scalar loads / stores: data read or written once.
-template <typename T>
-__device__ __forceinline__ T ldg_nt(const T* p) { return __builtin_nontemporal_load(p); }
-template <typename T>
-__device__ __forceinline__ void stg_nt(T* p, T v) { __builtin_nontemporal_store(v, p); }
 
 // Unpack 16 bytes into floats: 4 fp32 or 8 bf16.
 __device__ __forceinline__ void unpack16(u32x4 r, float* out, float /*tag*/) {
