@@ -121,10 +121,14 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
 // loads are in flight through form_L and the inversion; the k tile is staged
 // in LDS and the MFMA fragments are read from there.  The arithmetic is the
 // one-tile kernel's, so A is bit-identical.
-constexpr int kABPipeWGsPerCU = 3;
+// Workgroups per CU: 3 for K = 64 (137 VGPRs); for K = 128 the 168-register
+// cap of 3 made the compiler spill, and 2 measured faster (149 against 153 us
+// at config 4; K = 64: 107 us at 3 against 135 at 2).
+template <int K>
+constexpr int ab_pipe_wgs_per_cu() { return K == 128 ? 2 : 3; }
 
 template <int K, int SIGN>
-__global__ void __launch_bounds__(kABThreads, kABPipeWGsPerCU)
+__global__ void __launch_bounds__(kABThreads, ab_pipe_wgs_per_cu<K>())
 wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ beta,
                        const float* __restrict__ g, float* __restrict__ A, int64_t T, int64_t H,
                        int64_t NT, int64_t tiles) {
@@ -213,7 +217,7 @@ hipError_t launch_A(const void* k, const void* beta, const void* g, void* A, int
   const int64_t NT = T / kBT;
   const int64_t tiles = B * NT * H;
   if constexpr (std::is_same<IT, bf16>::value) {
-    const int64_t pgrid = (int64_t)device_cu_count() * kABPipeWGsPerCU;
+    const int64_t pgrid = (int64_t)device_cu_count() * ab_pipe_wgs_per_cu<K>();
     if (pgrid > 0 && tiles >= 2 * pgrid) {
       if (sign < 0)
         hipLaunchKernelGGL((wy_build_A_pipe_kernel<K, -1>), dim3((unsigned)pgrid), dim3(kABThreads), 0, s,
