@@ -11,16 +11,20 @@ the kernels are launched on (torch's current stream), averaged over the timed
 steps.  ``roofline`` is for the kernel with the largest share of the step:
 algorithmic bytes per launch / its average duration vs 8 TB/s.  ``traffic``
 is read from profiles/traffic_cfg4.json when that summary of rocprofv3
-FETCH_SIZE / WRITE_SIZE runs exists, else null.  ``cpu_baseline`` times the
-CPU oracle on a bounded sample (one batch element of the same workload) and
-scales to a full step.  ``floors`` times memory-only kernels that move each
-step kernel's algorithmic bytes in its own tile pattern with no compute
-(theorem_amd/csrc/floors.hip): the fastest this box moves those bytes in that
-pattern, reported per kernel as ``floor_us`` and ``of_floor`` (floor / kernel
-time) beside the 8 TB/s roofline.  ``shapes`` gives each kernel's latency at configs 0-3,
-the shapes the reference publishes numbers for; ``extensions`` times the
+FETCH_SIZE / WRITE_SIZE runs exists, else null. ``cpu_baseline`` times the CPU
+oracle on a bounded sample (batch elements of the same workload, as many as
+fit in about 12 s) and scales to a full step. ``floors`` times memory-only
+kernels that move each step kernel's algorithmic bytes in its own tile pattern
+with no compute (theorem_amd/csrc/floors.hip): the fastest this box moves
+those bytes in that pattern, reported per kernel as ``floor_us`` and
+``of_floor`` (floor / kernel time) beside the 8 TB/s roofline.
+``measured_peaks`` gives the box's copy rate and bf16 MFMA throughput (a
+register-only MFMA loop); each kernel's ``mfma_frac_of_measured`` is its flop
+rate against the latter. ``shapes`` gives each kernel's latency at configs
+0-3, the shapes the reference publishes numbers for; ``extensions`` times the
 kernels beyond the four (WY matrix, gate cumsum, channels-last conv, conv
-decode step) at config-4 sizes.
+decode step, fused WY, fused h + o, the whole chunked forward) at config-4
+sizes.
 """
 from __future__ import annotations
 
@@ -254,6 +258,48 @@ def pattern_floors(torch, inp, conv_in, reps: int = 5):
     return out
 
 
+def measured_peaks(torch, dev, floors, reps: int = 5):
+    """Peaks taken on this box beside the published ones: the streaming-copy
+    rate (the conv's floor, a copy of x) and the bf16 MFMA throughput of
+    floor_mfma_kernel (libtheorem_floors.so: v_mfma_f32_16x16x32_bf16 on register
+    operands, no memory traffic; 8 workgroups of 4 waves per CU, 16 independent
+    accumulator chains per wave), min over ``reps`` launches."""
+    import ctypes
+
+    from theorem_amd.build import FLOORS_LIB
+
+    if not FLOORS_LIB.exists():
+        return None
+    lib = ctypes.CDLL(str(FLOORS_LIB))
+    nblocks = 8 * torch.cuda.get_device_properties(dev).multi_processor_count
+    iters, chains = 2048, 16
+    out = torch.empty(nblocks * 256, device=dev, dtype=torch.float32)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def run():
+        return lib.thm_floor_mfma(ctypes.c_void_p(out.data_ptr()), ctypes.c_int64(nblocks), ctypes.c_int64(iters),
+                                  stream)
+
+    if run() != 0:
+        return None
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3)
+    flops = nblocks * 4 * iters * chains * 16384
+    res = {"mfma_bf16_TFLOPs": round(flops / best / 1e6, 1),
+           "mfma_of_published": round(flops / (best * 1e-6) / MFMA_BF16_PEAK, 3)}
+    if floors and "causal_conv1d" in floors:
+        res["copy_GBps"] = floors["causal_conv1d"]["GBps"]
+        res["copy_of_published"] = round(floors["causal_conv1d"]["GBps"] * 1e9 / HBM_PEAK, 3)
+    return res
+
+
 def work_build_A(B, T, H, K, eb=2):
     N = B * T * H
     return N * K * eb + N * 8 + N * 64 * 4
@@ -447,7 +493,7 @@ def main() -> int:
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
                 "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic}
 
-    floors = None
+    floors = peaks = None
     if not args.small:
         print("[bench] memory-only pattern floors", file=sys.stderr, flush=True)
         floors = pattern_floors(torch, inp, conv_in)
@@ -455,6 +501,13 @@ def main() -> int:
             for n in names:
                 kernels[n]["floor_us"] = floors[n]["us"]
                 kernels[n]["of_floor"] = round(floors[n]["us"] / kernels[n]["us"], 3)
+        print("[bench] measured peaks (copy, bf16 MFMA)", file=sys.stderr, flush=True)
+        peaks = measured_peaks(torch, inp["k"].device, floors)
+        if peaks:
+            for n in names:
+                _, fl = works[n]
+                kernels[n]["mfma_frac_of_measured"] = round(
+                    fl / (kernels[n]["us"] * 1e-6) / (peaks["mfma_bf16_TFLOPs"] * 1e12), 4)
 
     shapes = None
     if not args.no_shapes:
@@ -483,7 +536,8 @@ def main() -> int:
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded torch CPU generator; BASELINE.json config-4 distributions)",
         "config": {"workload": workload, "parallelism": "single GPU"},
-        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu, "floors": floors, "shapes": shapes,
+        "kernels": kernels, "roofline": roofline, "cpu_baseline": cpu, "floors": floors, "measured_peaks": peaks,
+        "shapes": shapes,
         "extensions": ext,
     }
     print(json.dumps(line))

@@ -42,7 +42,8 @@ def test_floors_library_loads_and_rejects_bad_calls():
     from theorem_amd.build import FLOORS_LIB
 
     lib = ctypes.CDLL(str(FLOORS_LIB))
-    for name in ("thm_floor_copy", "thm_floor_wu", "thm_floor_h", "thm_floor_o", "thm_floor_wy", "thm_floor_ho"):
+    for name in ("thm_floor_copy", "thm_floor_wu", "thm_floor_h", "thm_floor_o", "thm_floor_wy", "thm_floor_ho",
+                 "thm_floor_mfma"):
         assert hasattr(lib, name), name
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     assert lib.thm_floor_copy(vp(FAKE), vp(FAKE), i64(17), None) == -1  # not a multiple of 16
@@ -50,6 +51,9 @@ def test_floors_library_loads_and_rejects_bad_calls():
                            i64(1), i64(100), i64(2), None) == -1  # T % 64 != 0
     assert lib.thm_floor_o(None, vp(FAKE), vp(FAKE), vp(FAKE), vp(FAKE), vp(FAKE),
                            i64(1), i64(64), i64(2), None) == -1  # NULL input
+    assert lib.thm_floor_mfma(None, i64(4), i64(16), None) == -1  # NULL output
+    assert lib.thm_floor_mfma(vp(FAKE), i64(0), i64(16), None) == -1  # empty grid
+    assert lib.thm_floor_mfma(vp(FAKE), i64(4), i64(0), None) == -1  # no iterations
 
 
 def test_abi_version_and_status_strings():

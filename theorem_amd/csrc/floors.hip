@@ -17,12 +17,18 @@
 // One 256-thread workgroup per (b, chunk of 64 tokens, head) tile, head
 // fastest, every load of the tile issued before the first store, as the
 // tile-parallel hot-path kernels do.  Outputs hold XOR mixes of the inputs.
+//
+// A second reference point, floor_mfma_kernel, measures the box's bf16 MFMA
+// throughput (v_mfma_f32_16x16x32_bf16 on register operands, no memory
+// traffic) for the compute side of the roofline.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kRow = 256;      // bytes per token-head row of every [B, T, H, 128] bf16 tensor
 constexpr int kHTile = 65536;  // bytes of one fp32 128 x 128 state
@@ -61,6 +67,33 @@ __global__ void __launch_bounds__(256) floor_copy_kernel(const char* __restrict_
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (i0 + i * 256 < n16) __builtin_nontemporal_store(r[i], (u32x4*)(dst + (i0 + i * 256) * 16));
+}
+
+// bf16 MFMA throughput: each wave runs kMfmaChains independent accumulator
+// chains of v_mfma_f32_16x16x32_bf16 (16384 flops each) for `iters` rounds,
+// then writes one sum per lane so nothing is dead code.  16 chains: with 8
+// the MFMA pipe waits on each chain's accumulator (1.2-1.4 PFLOP/s on the box
+// against 2.0-2.1 with 16 at 2-8 waves per SIMD).
+constexpr int kMfmaChains = 16;
+__global__ void __launch_bounds__(256) floor_mfma_kernel(float* __restrict__ out, int64_t iters) {
+  const int lane = threadIdx.x & 63;
+  bf16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (__bf16)(1e-3f * (float)(lane + i));
+    b[i] = (__bf16)(1e-3f * (float)(lane - i));
+  }
+  f32x4 acc[kMfmaChains];
+#pragma unroll
+  for (int c = 0; c < kMfmaChains; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int c = 0; c < kMfmaChains; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[c], 0, 0, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < kMfmaChains; ++c) sum += acc[c][0] + acc[c][1] + acc[c][2] + acc[c][3];
+  out[(int64_t)blockIdx.x * 256 + threadIdx.x] = sum;
 }
 
 // recompute_w_u: k, v, A rows, beta, g in; w, u rows out.
@@ -204,6 +237,15 @@ extern "C" int thm_floor_copy(const void* src, void* dst, int64_t nbytes, void* 
   const int64_t n16 = nbytes / 16, per_block = 256 * 4;
   hipLaunchKernelGGL(floor_copy_kernel, dim3((unsigned)((n16 + per_block - 1) / per_block)), dim3(256), 0,
                      (hipStream_t)stream, (const char*)src, (char*)dst, n16);
+  return (int)hipGetLastError();
+}
+
+// bf16 MFMA throughput: `nblocks` workgroups of 256 threads (out holds
+// nblocks * 256 floats); flops = nblocks * 4 waves * iters * kMfmaChains * 16384.
+extern "C" int thm_floor_mfma(void* out, int64_t nblocks, int64_t iters, void* stream) {
+  if (!out || nblocks <= 0 || nblocks > (INT64_C(1) << 31) - 1 || iters <= 0 || (uintptr_t)out % 4) return -1;
+  hipLaunchKernelGGL(floor_mfma_kernel, dim3((unsigned)nblocks), dim3(256), 0, (hipStream_t)stream, (float*)out,
+                     iters);
   return (int)hipGetLastError();
 }
 
