@@ -105,6 +105,24 @@ def test_chunk_fwd_h_validation():
     assert h(B=0) == 0
 
 
+def test_prep_gives_dense_aligned_tensors():
+    """The wrappers' layout step: dense 16-byte aligned tensors pass through
+    untouched; strided or misaligned ones become dense aligned copies with the
+    same values."""
+    x = torch.arange(64, dtype=torch.float32).reshape(4, 16)
+    assert _capi.prep(x, "x") is x
+    s = x[:, ::2]
+    ps = _capi.prep(s, "s")
+    assert ps.is_contiguous() and torch.equal(ps, s)
+    flat = torch.zeros(80, dtype=torch.float32)
+    off = flat[1:65].view(4, 16)
+    off.copy_(x)
+    if off.data_ptr() % 16:
+        po = _capi.prep(off, "off")
+        assert po.data_ptr() % 16 == 0 and torch.equal(po, x)
+    assert _capi.prep(None, "none") is None
+
+
 def test_python_wrapper_rejects_cpu_tensors():
     from theorem_amd.kernels.causal_conv1d import custom_kernel
     x = torch.zeros(1, 4, 8)

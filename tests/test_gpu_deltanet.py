@@ -354,3 +354,51 @@ def test_chain_matches_token_recurrence(dev, K, V, gate):
     eo, eS = odn.gated_delta_rule_tokens(np_(q), np_(k), np_(v), np_(beta), np_(a), scale)
     assert_close(o, eo, 1e-2, 1e-2, f"chain o {gate}")
     assert_close(ht, eS, 1e-2, 1e-2, f"chain final state {gate}")
+
+
+# --------------------------------------------------------------------------- strided and offset views
+
+def _strided(t):
+    """A non-contiguous view holding t's values: every other element along the
+    last dimension of a tensor twice as wide."""
+    wide = torch.zeros(*t.shape[:-1], 2 * t.shape[-1], dtype=t.dtype, device=t.device)
+    wide[..., ::2] = t
+    return wide[..., ::2]
+
+
+def _offset(t):
+    """A contiguous view holding t's values whose data pointer sits 4 bytes past
+    a 16-byte boundary."""
+    n, e = t.numel(), 4 // t.element_size()
+    flat = torch.zeros(n + 16, dtype=t.dtype, device=t.device)
+    assert flat.data_ptr() % 16 == 0
+    flat[e:e + n] = t.reshape(-1)
+    return flat[e:e + n].view(t.shape)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("view", [_strided, _offset])
+def test_wrappers_take_strided_and_offset_views(dev, dtype, view):
+    """The three wrappers accept non-contiguous and misaligned inputs (copied to
+    dense 16-byte aligned tensors before the C ABI call) and return exactly
+    what the dense inputs give."""
+    d = configs.make_wu_inputs(1, 128, 2, 64, 64, seed=3, device=dev, dtype=dtype)
+    vw = {n: view(t) for n, t in d.items()}
+    assert not vw["k"].is_contiguous() or vw["k"].data_ptr() % 16
+    ref = recompute_w_u.custom_kernel(recompute_w_u.Data(**d, B=1, T=128, H=2, K=64, V=64))
+    got = recompute_w_u.custom_kernel(recompute_w_u.Data(**vw, B=1, T=128, H=2, K=64, V=64))
+    sync()
+    assert all(torch.equal(a, b) for a, b in zip(ref, got)), "recompute_w_u"
+
+    d = configs.make_o_inputs(1, 128, 2, 64, 128, seed=4, device=dev, dtype=dtype)
+    ref = chunk_fwd_o.custom_kernel(d)
+    got = chunk_fwd_o.custom_kernel({**{n: view(d[n]) for n in ("q", "k", "v", "g", "h")}, "scale": d["scale"]})
+    sync()
+    assert torch.equal(ref, got), "chunk_fwd_o"
+
+    d = configs.make_h_inputs(1, 256, 2, 64, 64, seed=5, device=dev, dtype=dtype, h0_std=0.1)
+    keys = dict(k="k", w="w", u="u", g="g", initial_state="h0")
+    ref = chunk_fwd_h.custom_kernel({**{a: d[b] for a, b in keys.items()}, "output_final_state": True})
+    got = chunk_fwd_h.custom_kernel({**{a: view(d[b]) for a, b in keys.items()}, "output_final_state": True})
+    sync()
+    assert all(torch.equal(a, b) for a, b in zip(ref, got)), "chunk_fwd_h"
