@@ -633,11 +633,18 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
       }
       if constexpr (STORE_VN) {
         bf16* vb = vnew + ((b * T + c * kBT) * H + hh) * V;
+        // Row tiles kJbStore kh .. + kJbStore - 1.  One branch per K half
+        // (kh is wave-uniform) keeps the register indices static: indexing
+        // vn by kh itself compiled to relative register moves.
+        auto store_vn = [&](auto kh_c) {
 #pragma unroll
-        for (int jj = 0; jj < C::kJbStore; ++jj) {
-          const int jb = C::kJbStore * kh + jj;
-          st_b64(vb, vnoff0 + (uint32_t)(16 * jb * tsv), acc_to_row_quads_bf16(vn[jb]));
-        }
+          for (int jj = 0; jj < C::kJbStore; ++jj) {
+            constexpr int kOff = C::kJbStore * decltype(kh_c)::value;
+            st_b64(vb, vnoff0 + (uint32_t)(16 * (kOff + jj) * tsv), acc_to_row_quads_bf16(vn[kOff + jj]));
+          }
+        };
+        if (kh == 0) store_vn(std::integral_constant<int, 0>{});
+        else if constexpr (KS == 2) store_vn(std::integral_constant<int, 1>{});
       }
     }
 
