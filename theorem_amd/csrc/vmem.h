@@ -90,12 +90,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Transpose the 4x4 matrix held by each quad of lanes (lane 4m + q holds row q
 // in v[0..3]): afterwards lane 4m + q holds column q, i.e. r[i] = the v[q] of
-// lane 4m + i.  Two DPP butterfly steps (quad_perm xor 1, xor 2).
+// lane 4m + i.  Two DPP butterfly steps (quad_perm xor 1, xor 2).  Every lane
+// of every row and bank is written from a lane of its own quad, so the DPP's
+// "old" operand is never observed: mov_dpp leaves it undefined, where
+// update_dpp with old = 0 cost a v_mov of 0 into each destination.
 __device__ __forceinline__ float dpp_quad_xor1(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
 }
 __device__ __forceinline__ float dpp_quad_xor2(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
 }
 __device__ __forceinline__ f32x4 quad_transpose(f32x4 v) {
   const int q = lane_id() & 3;
