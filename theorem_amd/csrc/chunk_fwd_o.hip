@@ -86,12 +86,9 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
   bf16* const vlo = lds + C::kVTile + C::kHTile;
   bf16* const hlo = vlo + C::kVTile;
 
-  const int64_t tile = blockIdx.x;
-  const int64_t hh = tile % H;
-  const int64_t bc = tile / H;
-  const int64_t c = bc % NT;
-  const int64_t b = bc / NT;
-  const int64_t tok0 = b * T + c * kBT;
+  const TileCoord tc = tile_coord(blockIdx.x, H, NT, T);
+  const int64_t hh = tc.hh;
+  const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
   const int lane = tid & 63;
@@ -109,7 +106,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     const int col = (qi - j * C::kVCPR) * C::kVE;
     vr[it] = ldg16_nt(v + ((tok0 + j) * H + hh) * V + col);
   }
-  const float* hsrc = hs + ((b * NT + c) * H + hh) * (int64_t)(K * V);
+  const float* hsrc = hs + (int64_t)blockIdx.x * (K * V);  // h[b, c, hh]: the state of this tile
 #pragma unroll
   for (int it = 0; it < C::kHLoads; ++it) {
     const int qi = tid + it * kOThreads;
@@ -289,10 +286,9 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 
   // Tile -> (b, c, head), head fastest (as the one-tile kernel).
   auto tok_of = [&](int64_t tile, int64_t& hh) {
-    hh = tile % H;
-    const int64_t bc = tile / H;
-    const int64_t c = bc % NT, b = bc / NT;
-    return b * T + c * kBT;
+    const TileCoord tc = tile_coord(tile, H, NT, T);
+    hh = tc.hh;
+    return tc.tok0;
   };
 
   // Prefetched registers of one tile.

@@ -60,6 +60,19 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Head index and first token row of tile `tile` of a [B, T / 64, H] tile
+// grid with the head fastest.  Every entry point that uses it checks that the
+// tile count is below 2^31, so 32-bit unsigned division is exact; it replaces
+// the 64-bit division sequences of int64_t % and /.
+struct TileCoord {
+  int64_t hh, tok0;
+};
+__device__ __forceinline__ TileCoord tile_coord(int64_t tile, int64_t H, int64_t NT, int64_t T) {
+  const uint32_t t = (uint32_t)tile, h = (uint32_t)H, nt = (uint32_t)NT;
+  const uint32_t bc = t / h, b = bc / nt;
+  return {(int64_t)(t - bc * h), (int64_t)b * T + (int64_t)(bc - b * nt) * 64};
+}
+
 // Compute units of the current device (queried once per device, then cached;
 // 0 if the query fails).  Used to size persistent grids.
 inline int device_cu_count() {

@@ -57,12 +57,9 @@ recompute_w_u_kernel(const IT* __restrict__ k, const IT* __restrict__ v,
 
   // tile -> (b, c, h) with the head fastest: consecutive workgroups read one
   // contiguous [64 tokens x H x D] block.
-  const int64_t tile = blockIdx.x;
-  const int64_t h = tile % H;
-  const int64_t bc = tile / H;
-  const int64_t c = bc % NT;
-  const int64_t b = bc / NT;
-  const int64_t tok0 = b * T + c * kBT;
+  const TileCoord tc = tile_coord(blockIdx.x, H, NT, T);
+  const int64_t h = tc.hh;
+  const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
   const int lane = tid & 63;

@@ -69,12 +69,9 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
   __shared__ float Tb[3 * kBlk];   // per-level partial products
   __shared__ float sb[kBT], sg[kBT];
 
-  const int64_t tile = blockIdx.x;
-  const int64_t h = tile % H;
-  const int64_t bc = tile / H;
-  const int64_t c = bc % NT;
-  const int64_t b = bc / NT;
-  const int64_t tok0 = b * T + c * kBT;
+  const TileCoord tc = tile_coord(blockIdx.x, H, NT, T);
+  const int64_t h = tc.hh;
+  const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
   const int lane = tid & 63;
@@ -149,9 +146,9 @@ wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ bet
   const int grp = lane >> 4, li = lane & 15;
 
   auto tok_of = [&](int64_t tile, int64_t& h) {
-    h = tile % H;
-    const int64_t bc = tile / H;
-    return (bc / NT) * T + (bc % NT) * kBT;
+    const TileCoord tc = tile_coord(tile, H, NT, T);
+    h = tc.hh;
+    return tc.tok0;
   };
   u32x4 kr[kLoads];
   float br = 0.f, gr = 0.f;

@@ -115,12 +115,9 @@ wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
   float* const Tb = Xb + 10 * kBlk;                  // per-level partial products
   bf16* const xs = reinterpret_cast<bf16*>(lds);    // [k | v] tile, after the inversion
 
-  const int64_t tile = blockIdx.x;
-  const int64_t h = tile % H;
-  const int64_t bc = tile / H;
-  const int64_t c = bc % NT;
-  const int64_t b = bc / NT;
-  const int64_t tok0 = b * T + c * kBT;
+  const TileCoord tc = tile_coord(blockIdx.x, H, NT, T);
+  const int64_t h = tc.hh;
+  const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
   const int wv = tid >> 6;
   const int lane = tid & 63;
@@ -212,9 +209,9 @@ wy_fwd_pipe_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
 
   // Tile -> (b, c, head), head fastest.
   auto tok_of = [&](int64_t tile, int64_t& h) {
-    h = tile % H;
-    const int64_t bc = tile / H;
-    return (bc / NT) * T + (bc % NT) * kBT;
+    const TileCoord tc = tile_coord(tile, H, NT, T);
+    h = tc.hh;
+    return tc.tok0;
   };
 
   // Prefetched registers of one tile (thread q: row q / kCPR, 16-byte chunk q % kCPR).
