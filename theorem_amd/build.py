@@ -30,12 +30,24 @@ SOURCES = [
     "causal_conv1d_ext.hip",
     "recompute_w_u.hip",
     "chunk_fwd_h.hip",
+    "chunk_fwd_h_f32.hip",
     "chunk_fwd_o.hip",
     "chunk_fwd_fused.hip",
     "wy_build_A.hip",
     "wy_fwd.hip",
     "gates.hip",
 ]
+
+# Per-unit code generation.  Forcing MFMA accumulators into VGPRs (no AGPR
+# copies) measured faster for these units (recompute_w_u bf16 275.1 -> 271.6 us,
+# the bf16 register chunk_fwd_h at config 3 25.5 -> 24.4 us, config 4
+# bit-identical outputs) and slower for the fp32 register chunk_fwd_h and the
+# fp32 chunk_fwd_o (775 -> 884 and 883 -> 927 us), so it is not global.
+MFMA_VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+UNIT_FLAGS = {
+    "recompute_w_u.hip": MFMA_VGPR_FORM,
+    "chunk_fwd_h.hip": MFMA_VGPR_FORM,
+}
 
 FLOORS_SRC = "floors.hip"
 FLOORS_LIB = LIB_DIR / "libtheorem_floors.so"
@@ -80,7 +92,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [
-            ex.submit(_run, [HIPCC, *COMMON_FLAGS, "-c", str(s), "-o", str(o)], verbose)
+            ex.submit(_run, [HIPCC, *COMMON_FLAGS, *UNIT_FLAGS.get(s.name, []), "-c", str(s), "-o", str(o)], verbose)
             for s, o in zip(srcs, objs)
         ]
         for f in futs:
