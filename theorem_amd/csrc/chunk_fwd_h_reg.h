@@ -141,7 +141,7 @@ chunk_fwd_h_kernel(const IT* __restrict__ k, const IT* __restrict__ w, const IT*
   };
 
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int lane = tid & 63;
   const int grp = lane >> 4;
   const int li = lane & 15;

@@ -90,7 +90,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
   const int64_t hh = tc.hh;
   const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int lane = tid & 63;
   const int grp = lane >> 4;
   const int li = lane & 15;
@@ -278,7 +278,7 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   __shared__ float gs[kBT];
 
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int lane = tid & 63;
   const int grp = lane >> 4;
   const int li = lane & 15;

@@ -61,7 +61,7 @@ recompute_w_u_kernel(const IT* __restrict__ k, const IT* __restrict__ v,
   const int64_t h = tc.hh;
   const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int lane = tid & 63;
   const int grp = lane >> 4;
   const int li = lane & 15;

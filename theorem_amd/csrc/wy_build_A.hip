@@ -73,7 +73,7 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
   const int64_t h = tc.hh;
   const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int lane = tid & 63;
   const int grp = lane >> 4, li = lane & 15;
 
@@ -141,7 +141,7 @@ wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ bet
   __shared__ float sb[kBT], sg[kBT];
 
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int lane = tid & 63;
   const int grp = lane >> 4, li = lane & 15;
 

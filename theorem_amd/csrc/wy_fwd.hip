@@ -119,7 +119,7 @@ wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
   const int64_t h = tc.hh;
   const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int lane = tid & 63;
   const int grp = lane >> 4, li = lane & 15;
 
@@ -203,7 +203,7 @@ wy_fwd_pipe_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
   __shared__ float sb[kBT], sg[kBT];
 
   const int tid = threadIdx.x;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
   const int lane = tid & 63;
   const int grp = lane >> 4, li = lane & 15;
 
