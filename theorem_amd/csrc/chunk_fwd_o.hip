@@ -6,10 +6,14 @@
 // factored gates q e^{g}, v e^{-g}.  Here only e^{g_i - g_j} with j <= i is
 // formed, which cannot overflow for a non-increasing gate.
 //
-// One workgroup (4 wavefronts) per (b, chunk, head) tile, one memory phase:
-// every global load of the tile (v_c, h[c], this wave's q rows and the k rows
-// of its key blocks, g) is issued before the first wait.  v_c [64 x V] and
-// h[c] [K x V] are then staged in LDS as bf16 (fp32 inputs: bf16 hi + lo).
+// Three kernels: for bf16 inputs, the one-tile kernel below and, on grids
+// of two or more tiles per persistent workgroup, a software-pipelined form;
+// for fp32 inputs, chunk_fwd_o_f32_kernel (q h on fp32 MFMA, further below).
+//
+// One-tile kernel: one workgroup (4 wavefronts) per (b, chunk, head) tile,
+// one memory phase: every global load of the tile (v_c, h[c], this wave's q
+// rows and the k rows of its key blocks, g) is issued before the first wait.
+// v_c [64 x V] and h[c] [K x V] are then staged in LDS as bf16.
 // Wave wv owns query positions i = 16 wv .. 16 wv + 15 and computes o^T
 // (features x positions), so each lane ends with 4 consecutive features of
 // one token:
@@ -30,61 +34,30 @@ namespace {
 constexpr int kBT = 64;
 constexpr int kOThreads = 256;
 
-template <typename IT, int K, int V>
+template <int K, int V>
 struct OCfg {
-  static constexpr bool kSplit = std::is_same<IT, float>::value;
   static constexpr int kPitch = V + 8;  // LDS row pitch (elements) of the v and h tiles
   static constexpr int kVTile = kBT * kPitch;
   static constexpr int kHTile = K * kPitch;
-  static constexpr int kLds = (kSplit ? 2 : 1) * (kVTile + kHTile);
-  static constexpr int kVE = 16 / (int)sizeof(IT);
-  static constexpr int kVCPR = V / kVE;                         // 16-byte chunks per v row
+  static constexpr int kLds = kVTile + kHTile;
+  static constexpr int kVCPR = V / 8;                           // 16-byte chunks per v row
   static constexpr int kVLoads = kBT * kVCPR / kOThreads;
   static constexpr int kHLoads = K * (V / 4) / kOThreads;       // h is fp32
   static constexpr int KS = K / 32;                             // contraction steps over K
-  static constexpr int kFragLoads = kSplit ? 2 : 1;             // 16-byte loads per 8-element fragment
   static_assert(kBT * kVCPR % kOThreads == 0 && K * (V / 4) % kOThreads == 0, "staging split");
 };
 
-// 8 elements of a q / k row as an MFMA fragment (fp32: raw, split at use).
-template <typename IT>
-struct RowFrag {
-  u32x4 r[sizeof(IT) == 4 ? 2 : 1];
-};
-
-template <typename IT>
-__device__ __forceinline__ RowFrag<IT> load_frag(const IT* p) {
-  RowFrag<IT> f;
-  f.r[0] = ldg16_nt(p);
-  if constexpr (sizeof(IT) == 4) f.r[1] = ldg16_nt(p + 4);
-  return f;
-}
-
-template <typename IT>
-__device__ __forceinline__ void frag_bf16(const RowFrag<IT>& f, bf16x8& hi, bf16x8& lo) {
-  if constexpr (sizeof(IT) == 4) {
-    float v[8];
-    unpack16(f.r[0], v, 0.f);
-    unpack16(f.r[1], v + 4, 0.f);
-    split_bf16x8(v, hi, lo);
-  } else {
-    hi = __builtin_bit_cast(bf16x8, f.r[0]);
-  }
-}
-
-template <typename IT, int K, int V>
+template <int K, int V>
 __global__ void __launch_bounds__(kOThreads)
-chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT* __restrict__ v,
-                   const float* __restrict__ g, const float* __restrict__ hs, IT* __restrict__ o,
+chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+                   const float* __restrict__ g, const float* __restrict__ hs, bf16* __restrict__ o,
                    float scale, int64_t T, int64_t H, int64_t NT) {
-  using C = OCfg<IT, K, V>;
+  using C = OCfg<K, V>;
   constexpr int KS = C::KS;
   __shared__ __attribute__((aligned(16))) bf16 lds[C::kLds];
   __shared__ float gs[kBT];
   bf16* const vhi = lds;
   bf16* const hhi = lds + C::kVTile;
-  bf16* const vlo = lds + C::kVTile + C::kHTile;
-  bf16* const hlo = vlo + C::kVTile;
 
   const TileCoord tc = tile_coord(blockIdx.x, H, NT, T);
   const int64_t hh = tc.hh;
@@ -103,7 +76,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
   for (int it = 0; it < C::kVLoads; ++it) {
     const int qi = tid + it * kOThreads;
     const int j = qi / C::kVCPR;
-    const int col = (qi - j * C::kVCPR) * C::kVE;
+    const int col = (qi - j * C::kVCPR) * 8;
     vr[it] = ldg16_nt(v + ((tok0 + j) * H + hh) * V + col);
   }
   const float* hsrc = hs + (int64_t)blockIdx.x * (K * V);  // h[b, c, hh]: the state of this tile
@@ -115,31 +88,25 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     hr[it] = ldg16_nt(hsrc + r * V + col);
   }
   // q fragments q[i][32 s + 8 grp + 0..7] and k fragments of key blocks jb <= wv.
-  RowFrag<IT> qf[KS], kf[4][KS];
+  bf16x8 qh[KS], kf[4][KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) qf[s] = load_frag(q + qrow * K + 32 * s + 8 * grp);
+  for (int s = 0; s < KS; ++s) qh[s] = __builtin_bit_cast(bf16x8, ldg16_nt(q + qrow * K + 32 * s + 8 * grp));
 #pragma unroll
   for (int jb = 0; jb < 4; ++jb) {
     if (jb > wv) continue;  // wave-uniform
     const int64_t krow = (tok0 + 16 * jb + li) * H + hh;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) kf[jb][s] = load_frag(k + krow * K + 32 * s + 8 * grp);
+    for (int s = 0; s < KS; ++s) kf[jb][s] = __builtin_bit_cast(bf16x8, ldg16_nt(k + krow * K + 32 * s + 8 * grp));
   }
   const float gload = (tid < kBT && g) ? g[(tok0 + tid) * H + hh] : 0.f;
 
-  // 2. Stage v_c and h[c] as bf16 (hi[, lo]) and g.
+  // 2. Stage v_c and h[c] (as bf16) and g.
 #pragma unroll
   for (int it = 0; it < C::kVLoads; ++it) {
     const int qi = tid + it * kOThreads;
     const int j = qi / C::kVCPR;
-    const int col = (qi - j * C::kVCPR) * C::kVE;
-    if constexpr (C::kSplit) {
-      float vals[4];
-      unpack16(vr[it], vals, 0.f);
-      lds_put4(vhi + j * C::kPitch + col, vlo + j * C::kPitch + col, vals, true);
-    } else {
-      *reinterpret_cast<u32x4*>(vhi + j * C::kPitch + col) = vr[it];
-    }
+    const int col = (qi - j * C::kVCPR) * 8;
+    *reinterpret_cast<u32x4*>(vhi + j * C::kPitch + col) = vr[it];
   }
 #pragma unroll
   for (int it = 0; it < C::kHLoads; ++it) {
@@ -148,14 +115,10 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     const int col = (qi - r * (V / 4)) * 4;
     float vals[4];
     unpack16(hr[it], vals, 0.f);
-    lds_put4(hhi + r * C::kPitch + col, hlo + r * C::kPitch + col, vals, C::kSplit);
+    lds_put4(hhi + r * C::kPitch + col, nullptr, vals, false);
   }
   if (tid < kBT) gs[tid] = gload;
   lds_barrier();
-
-  bf16x8 qh[KS], ql[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) frag_bf16(qf[s], qh[s], ql[s]);
 
   // 3. Inter-chunk term, then scaled by e^{g_i}.
   constexpr int NB = V / 16;
@@ -168,11 +131,6 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
       const int r0 = tr_row_natural(32 * s, 0), r1 = tr_row_natural(32 * s, 1);
       const bf16x8 hf = frag_tr(hhi, C::kPitch, r0, r1, 16 * nb);
       acc[nb] = mfma16x16x32(hf, qh[s], acc[nb]);
-      if constexpr (C::kSplit) {
-        acc[nb] = mfma16x16x32(hf, ql[s], acc[nb]);
-        const bf16x8 hl = frag_tr(hlo, C::kPitch, r0, r1, 16 * nb);
-        acc[nb] = mfma16x16x32(hl, qh[s], acc[nb]);
-      }
     }
   }
   const float gi = gs[i];
@@ -187,15 +145,7 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
     p[jb] = zero4();
     if (jb > wv) continue;  // wave-uniform
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      bf16x8 kh, kl;
-      frag_bf16(kf[jb][s], kh, kl);
-      p[jb] = mfma16x16x32(kh, qh[s], p[jb]);
-      if constexpr (C::kSplit) {
-        p[jb] = mfma16x16x32(kh, ql[s], p[jb]);
-        p[jb] = mfma16x16x32(kl, qh[s], p[jb]);
-      }
-    }
+    for (int s = 0; s < KS; ++s) p[jb] = mfma16x16x32(kf[jb][s], qh[s], p[jb]);
     // lane holds S^T[j = 16 jb + 4 grp + r][i]
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -208,25 +158,12 @@ chunk_fwd_o_kernel(const IT* __restrict__ q, const IT* __restrict__ k, const IT*
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     if (2 * s > wv) continue;  // wave-uniform: both blocks fully masked
-    float f[8] = {p[2 * s][0], p[2 * s][1], p[2 * s][2], p[2 * s][3],
-                  p[2 * s + 1][0], p[2 * s + 1][1], p[2 * s + 1][2], p[2 * s + 1][3]};
-    bf16x8 ph, pl;
-    if constexpr (C::kSplit) {
-      split_bf16x8(f, ph, pl);
-    } else {
-      ph = to_bf16x8(f);
-    }
+    const float f[8] = {p[2 * s][0], p[2 * s][1], p[2 * s][2], p[2 * s][3],
+                        p[2 * s + 1][0], p[2 * s + 1][1], p[2 * s + 1][2], p[2 * s + 1][3]};
+    const bf16x8 ph = to_bf16x8(f);
     const int r0 = tr_row_paired(32 * s, 0), r1 = tr_row_paired(32 * s, 1);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const bf16x8 vf = frag_tr(vhi, C::kPitch, r0, r1, 16 * nb);
-      acc[nb] = mfma16x16x32(vf, ph, acc[nb]);
-      if constexpr (C::kSplit) {
-        acc[nb] = mfma16x16x32(vf, pl, acc[nb]);
-        const bf16x8 vl = frag_tr(vlo, C::kPitch, r0, r1, 16 * nb);
-        acc[nb] = mfma16x16x32(vl, ph, acc[nb]);
-      }
-    }
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16x16x32(frag_tr(vhi, C::kPitch, r0, r1, 16 * nb), ph, acc[nb]);
   }
 
   // 6. o[i][16 nb + 4 grp + 0..3].
@@ -421,13 +358,195 @@ hipError_t launch_o_pipe(const void* q, const void* k, const void* v, const void
   return hipGetLastError();
 }
 
-template <typename IT, int K, int V>
+// ---------------------------------------------------------------------------
+// fp32 inputs: the inter-chunk term on fp32 MFMA with h read from memory.
+//
+// Staging h as bf16 hi + lo beside v took 104 KB of LDS (one workgroup per
+// CU).  Here q h runs on v_mfma_f32_16x16x4_f32 (exact fp32 products): step
+// (a, e) contracts kappa = 32 a + 8 grp + e, whose A operand is the lane's
+// own q value (the q fragment layout) and whose B operand, h[kappa][16 nb +
+// li], is one float per lane read straight from memory (4 rows x 64 bytes per
+// instruction; the tile's 4 waves share h through L2).  Only v and k are
+// staged (bf16 hi + lo, 70 KB: two workgroups per CU).  Both products are
+// formed untransposed, D[i][n] (rows i = 16 wv + 4 grp + r, column n = 16 nb +
+// li): the intra-chunk term takes the score accumulator pairs as its A
+// operand and the v^T fragment as its B operand, the kernel above's operands
+// swapped.
+template <int K, int V>
+struct OFCfg {
+  static constexpr int kPitch = V + 8;   // v rows (bf16 elements, 16-byte pad)
+  static constexpr int kKPitch = K + 8;  // k rows
+  static constexpr int kVTile = kBT * kPitch;
+  static constexpr int kKTile = kBT * kKPitch;
+  static constexpr int kVLoads = kBT * (V / 4) / kOThreads;  // fp32 16-byte loads per thread
+  static constexpr int kKLoads = kBT * (K / 4) / kOThreads;
+  static constexpr int KS = K / 32;
+  static constexpr int NB = V / 16;
+  static_assert(kBT * (V / 4) % kOThreads == 0 && kBT * (K / 4) % kOThreads == 0, "staging split");
+};
+
+template <int K, int V>
+__global__ void __launch_bounds__(kOThreads, 2)
+chunk_fwd_o_f32_kernel(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+                       const float* __restrict__ g, const float* __restrict__ hs, float* __restrict__ o,
+                       float scale, int64_t T, int64_t H, int64_t NT) {
+  using C = OFCfg<K, V>;
+  constexpr int KS = C::KS, NB = C::NB;
+  __shared__ __attribute__((aligned(16))) bf16 lv[2 * C::kVTile];  // v hi, v lo
+  __shared__ __attribute__((aligned(16))) bf16 lk[2 * C::kKTile];  // k hi, k lo
+  __shared__ float gs[kBT];
+  bf16* const vhi = lv;
+  bf16* const vlo = lv + C::kVTile;
+  bf16* const khi = lk;
+  bf16* const klo = lk + C::kKTile;
+
+  const TileCoord tc = tile_coord(blockIdx.x, H, NT, T);
+  const int64_t hh = tc.hh;
+  const int64_t tok0 = tc.tok0;
+  const int tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: branches on it stay scalar
+  const int lane = tid & 63;
+  const int grp = lane >> 4;
+  const int li = lane & 15;
+  const int iq = 16 * wv + li;  // this lane's q row (A-operand row of both products)
+
+  // 1. Every load of the tile but h: v and k (16-byte pieces), this lane's q
+  // fragments q[iq][32 a + 8 grp + 0..7], g.
+  u32x4 vr[C::kVLoads], kr[C::kKLoads];
+#pragma unroll
+  for (int it = 0; it < C::kVLoads; ++it) {
+    const int qi = tid + it * kOThreads;
+    const int j = qi / (V / 4), col = (qi - j * (V / 4)) * 4;
+    vr[it] = ldg16_nt(v + ((tok0 + j) * H + hh) * V + col);
+  }
+#pragma unroll
+  for (int it = 0; it < C::kKLoads; ++it) {
+    const int qi = tid + it * kOThreads;
+    const int j = qi / (K / 4), col = (qi - j * (K / 4)) * 4;
+    kr[it] = ldg16_nt(k + ((tok0 + j) * H + hh) * K + col);
+  }
+  float qv[KS][8];
+#pragma unroll
+  for (int a = 0; a < KS; ++a) load8f(q + ((tok0 + iq) * H + hh) * K + 32 * a + 8 * grp, qv[a], true);
+  const float gload = (tid < kBT && g) ? g[(tok0 + tid) * H + hh] : 0.f;
+
+  // 2. Stage v and k as bf16 hi + lo, and g.
+#pragma unroll
+  for (int it = 0; it < C::kVLoads; ++it) {
+    const int qi = tid + it * kOThreads;
+    const int j = qi / (V / 4), col = (qi - j * (V / 4)) * 4;
+    float vals[4];
+    unpack16(vr[it], vals, 0.f);
+    lds_put4(vhi + j * C::kPitch + col, vlo + j * C::kPitch + col, vals, true);
+  }
+#pragma unroll
+  for (int it = 0; it < C::kKLoads; ++it) {
+    const int qi = tid + it * kOThreads;
+    const int j = qi / (K / 4), col = (qi - j * (K / 4)) * 4;
+    float vals[4];
+    unpack16(kr[it], vals, 0.f);
+    lds_put4(khi + j * C::kKPitch + col, klo + j * C::kKPitch + col, vals, true);
+  }
+  if (tid < kBT) gs[tid] = gload;
+
+  // 3. Inter-chunk term D[i][n] = sum_kappa q[i][kappa] h[kappa][n] (runs
+  // while the staging stores drain; h is not in LDS).
+  const float* hb = hs + (int64_t)blockIdx.x * (K * V) + li;  // h[b, c, hh]: the state of this tile
+  f32x4 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = zero4();
+#pragma unroll
+  for (int a = 0; a < KS; ++a)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float* hrow = hb + (32 * a + 8 * grp + e) * V;
+      float hv[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) hv[nb] = hrow[16 * nb];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[a][e], hv[nb], acc[nb], 0, 0, 0);
+    }
+  lds_barrier();
+  // acc[nb][r] holds row i = 16 wv + 4 grp + r: scale it by e^{g_i}.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float egi = fast_exp(gs[16 * wv + 4 * grp + r]);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb][r] *= egi;
+  }
+
+  // 4. Gated, causally masked scores S^T[j][iq] for key blocks jb <= wv (as
+  // the kernel above, with k from LDS).
+  bf16x8 qh[KS], ql[KS];
+#pragma unroll
+  for (int a = 0; a < KS; ++a) split_bf16x8(qv[a], qh[a], ql[a]);
+  const float gq = gs[iq];
+  f32x4 p[4];
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    p[jb] = zero4();
+    if (jb > wv) continue;  // wave-uniform
+#pragma unroll
+    for (int a = 0; a < KS; ++a) {
+      const int off = (16 * jb + li) * C::kKPitch + 32 * a + 8 * grp;
+      const bf16x8 kh = load8(khi + off), kl = load8(klo + off);
+      p[jb] = mfma16x16x32(kh, qh[a], p[jb]);
+      p[jb] = mfma16x16x32(kh, ql[a], p[jb]);
+      p[jb] = mfma16x16x32(kl, qh[a], p[jb]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * jb + 4 * grp + r;
+      p[jb][r] = (j <= iq) ? p[jb][r] * fast_exp(gq - gs[j]) : 0.f;
+    }
+  }
+
+  // 5. Intra-chunk term D[i][n] += sum_j P[i][j] v[j][n]: A = the score
+  // accumulator pairs (paired order over j), B = v^T fragments in the same order.
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    if (2 * s2 > wv) continue;  // wave-uniform: both key blocks fully masked
+    const float f[8] = {p[2 * s2][0], p[2 * s2][1], p[2 * s2][2], p[2 * s2][3],
+                        p[2 * s2 + 1][0], p[2 * s2 + 1][1], p[2 * s2 + 1][2], p[2 * s2 + 1][3]};
+    bf16x8 ph, pl;
+    split_bf16x8(f, ph, pl);
+    const int r0 = tr_row_paired(32 * s2, 0), r1 = tr_row_paired(32 * s2, 1);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const bf16x8 vh = frag_tr(vhi, C::kPitch, r0, r1, 16 * nb);
+      const bf16x8 vl = frag_tr(vlo, C::kPitch, r0, r1, 16 * nb);
+      acc[nb] = mfma16x16x32(ph, vh, acc[nb]);
+      acc[nb] = mfma16x16x32(pl, vh, acc[nb]);
+      acc[nb] = mfma16x16x32(ph, vl, acc[nb]);
+    }
+  }
+
+  // 6. o[i][16 nb + li] for i = 16 wv + 4 grp + r: 16 lanes cover 64 contiguous bytes of a row.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float* orow = o + ((tok0 + 16 * wv + 4 * grp + r) * H + hh) * V + li;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) orow[16 * nb] = acc[nb][r] * scale;
+  }
+}
+
+template <int K, int V>
+hipError_t launch_o_f32(const void* q, const void* k, const void* v, const void* g, const void* h, void* o,
+                        float scale, int64_t B, int64_t T, int64_t H, hipStream_t s) {
+  const int64_t NT = T / kBT;
+  hipLaunchKernelGGL((chunk_fwd_o_f32_kernel<K, V>), dim3((unsigned)(B * NT * H)), dim3(kOThreads), 0, s,
+                     (const float*)q, (const float*)k, (const float*)v, (const float*)g, (const float*)h,
+                     (float*)o, scale, T, H, NT);
+  return hipGetLastError();
+}
+
+template <int K, int V>
 hipError_t launch_o(const void* q, const void* k, const void* v, const void* g, const void* h,
                     void* o, float scale, int64_t B, int64_t T, int64_t H, hipStream_t s) {
   const int64_t NT = T / kBT;
-  hipLaunchKernelGGL((chunk_fwd_o_kernel<IT, K, V>), dim3((unsigned)(B * NT * H)), dim3(kOThreads),
-                     0, s, (const IT*)q, (const IT*)k, (const IT*)v, (const float*)g,
-                     (const float*)h, (IT*)o, scale, T, H, NT);
+  hipLaunchKernelGGL((chunk_fwd_o_kernel<K, V>), dim3((unsigned)(B * NT * H)), dim3(kOThreads),
+                     0, s, (const bf16*)q, (const bf16*)k, (const bf16*)v, (const float*)g,
+                     (const float*)h, (bf16*)o, scale, T, H, NT);
   return hipGetLastError();
 }
 
@@ -435,7 +554,12 @@ template <typename IT>
 hipError_t dispatch_o(int64_t K, int64_t V, const void* q, const void* k, const void* v,
                       const void* g, const void* h, void* o, float scale, int64_t B, int64_t T,
                       int64_t H, hipStream_t s) {
-  if constexpr (std::is_same<IT, bf16>::value) {
+  if constexpr (std::is_same<IT, float>::value) {
+    if (K == 64 && V == 64) return launch_o_f32<64, 64>(q, k, v, g, h, o, scale, B, T, H, s);
+    if (K == 64 && V == 128) return launch_o_f32<64, 128>(q, k, v, g, h, o, scale, B, T, H, s);
+    if (K == 128 && V == 64) return launch_o_f32<128, 64>(q, k, v, g, h, o, scale, B, T, H, s);
+    return launch_o_f32<128, 128>(q, k, v, g, h, o, scale, B, T, H, s);
+  } else {
     const int64_t tiles = B * (T / kBT) * H;
     const int64_t grid = (int64_t)device_cu_count() * kOPipeWGsPerCU;
     if (grid > 0 && tiles >= 2 * grid) {
@@ -444,11 +568,11 @@ hipError_t dispatch_o(int64_t K, int64_t V, const void* q, const void* k, const 
       if (K == 128 && V == 64) return launch_o_pipe<128, 64>(q, k, v, g, h, o, scale, B, T, H, grid, s);
       return launch_o_pipe<128, 128>(q, k, v, g, h, o, scale, B, T, H, grid, s);
     }
+    if (K == 64 && V == 64) return launch_o<64, 64>(q, k, v, g, h, o, scale, B, T, H, s);
+    if (K == 64 && V == 128) return launch_o<64, 128>(q, k, v, g, h, o, scale, B, T, H, s);
+    if (K == 128 && V == 64) return launch_o<128, 64>(q, k, v, g, h, o, scale, B, T, H, s);
+    return launch_o<128, 128>(q, k, v, g, h, o, scale, B, T, H, s);
   }
-  if (K == 64 && V == 64) return launch_o<IT, 64, 64>(q, k, v, g, h, o, scale, B, T, H, s);
-  if (K == 64 && V == 128) return launch_o<IT, 64, 128>(q, k, v, g, h, o, scale, B, T, H, s);
-  if (K == 128 && V == 64) return launch_o<IT, 128, 64>(q, k, v, g, h, o, scale, B, T, H, s);
-  return launch_o<IT, 128, 128>(q, k, v, g, h, o, scale, B, T, H, s);
 }
 
 }  // namespace
