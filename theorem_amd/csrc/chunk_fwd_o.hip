@@ -8,7 +8,7 @@
 //
 // Three kernels: for bf16 inputs, the one-tile kernel below and, on grids
 // of two or more tiles per persistent workgroup, a software-pipelined form;
-// for fp32 inputs, chunk_fwd_o_f32_kernel (q h on fp32 MFMA, further below).
+// for fp32 inputs, chunk_fwd_o_f32_kernel (h read from memory, further below).
 //
 // One-tile kernel: one workgroup (4 wavefronts) per (b, chunk, head) tile,
 // one memory phase: every global load of the tile (v_c, h[c], this wave's q
@@ -359,19 +359,19 @@ hipError_t launch_o_pipe(const void* q, const void* k, const void* v, const void
 }
 
 // ---------------------------------------------------------------------------
-// fp32 inputs: the inter-chunk term on fp32 MFMA with h read from memory.
+// fp32 inputs: the inter-chunk term with h read from memory.
 //
 // Staging h as bf16 hi + lo beside v took 104 KB of LDS (one workgroup per
-// CU).  Here q h runs on v_mfma_f32_16x16x4_f32 (exact fp32 products): step
-// (a, e) contracts kappa = 32 a + 8 grp + e, whose A operand is the lane's
-// own q value (the q fragment layout) and whose B operand, h[kappa][16 nb +
-// li], is one float per lane read straight from memory (4 rows x 64 bytes per
-// instruction; the tile's 4 waves share h through L2).  Only v and k are
-// staged (bf16 hi + lo, 70 KB: two workgroups per CU).  Both products are
-// formed untransposed, D[i][n] (rows i = 16 wv + 4 grp + r, column n = 16 nb +
-// li): the intra-chunk term takes the score accumulator pairs as its A
-// operand and the v^T fragment as its B operand, the kernel above's operands
-// swapped.
+// CU).  Here the B operand of q h, h[32 a + 8 grp + e][16 nb + li] for
+// e = 0..7, is read straight from memory as 8 floats per lane (4 rows x 64
+// bytes per instruction; the tile's 4 waves share h through L2), split into
+// bf16 hi + lo in registers, and contracted with the q fragments on
+// v_mfma_f32_16x16x32_bf16 (hi hi + lo hi + hi lo, as for every fp32 product
+// here).  Only v and k are staged (bf16 hi + lo, 70 KB at K = V = 128: two
+// workgroups per CU).  Both products are formed untransposed, D[i][n] (rows
+// i = 16 wv + 4 grp + r, column n = 16 nb + li): the intra-chunk term takes
+// the score accumulator pairs as its A operand and the v^T fragments as its
+// B operand, the one-tile kernel's operands swapped.
 template <int K, int V>
 struct OFCfg {
   static constexpr int kPitch = V + 8;   // v rows (bf16 elements, 16-byte pad)
@@ -450,21 +450,27 @@ chunk_fwd_o_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
   if (tid < kBT) gs[tid] = gload;
 
   // 3. Inter-chunk term D[i][n] = sum_kappa q[i][kappa] h[kappa][n] (runs
-  // while the staging stores drain; h is not in LDS).
+  // while the staging stores drain; h is not in LDS): kappa = 32 a + 8 grp + e
+  // in the q fragment's order.
   const float* hb = hs + (int64_t)blockIdx.x * (K * V) + li;  // h[b, c, hh]: the state of this tile
   f32x4 acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] = zero4();
+  bf16x8 qh[KS], ql[KS];
+#pragma unroll
+  for (int a = 0; a < KS; ++a) split_bf16x8(qv[a], qh[a], ql[a]);
 #pragma unroll
   for (int a = 0; a < KS; ++a)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float* hrow = hb + (32 * a + 8 * grp + e) * V;
-      float hv[NB];
+    for (int nb = 0; nb < NB; ++nb) {
+      float hv[8];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) hv[nb] = hrow[16 * nb];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[a][e], hv[nb], acc[nb], 0, 0, 0);
+      for (int e = 0; e < 8; ++e) hv[e] = hb[(32 * a + 8 * grp + e) * V + 16 * nb];
+      bf16x8 hh, hl;
+      split_bf16x8(hv, hh, hl);
+      acc[nb] = mfma16x16x32(qh[a], hh, acc[nb]);
+      acc[nb] = mfma16x16x32(ql[a], hh, acc[nb]);
+      acc[nb] = mfma16x16x32(qh[a], hl, acc[nb]);
     }
   lds_barrier();
   // acc[nb][r] holds row i = 16 wv + 4 grp + r: scale it by e^{g_i}.
@@ -477,9 +483,6 @@ chunk_fwd_o_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
 
   // 4. Gated, causally masked scores S^T[j][iq] for key blocks jb <= wv (as
   // the kernel above, with k from LDS).
-  bf16x8 qh[KS], ql[KS];
-#pragma unroll
-  for (int a = 0; a < KS; ++a) split_bf16x8(qv[a], qh[a], ql[a]);
   const float gq = gs[iq];
   f32x4 p[4];
 #pragma unroll
