@@ -362,16 +362,19 @@ hipError_t launch_o_pipe(const void* q, const void* k, const void* v, const void
 // fp32 inputs: the inter-chunk term with h read from memory.
 //
 // Staging h as bf16 hi + lo beside v took 104 KB of LDS (one workgroup per
-// CU).  Here the B operand of q h, h[32 a + 8 grp + e][16 nb + li] for
-// e = 0..7, is read straight from memory as 8 floats per lane (4 rows x 64
-// bytes per instruction; the tile's 4 waves share h through L2), split into
-// bf16 hi + lo in registers, and contracted with the q fragments on
-// v_mfma_f32_16x16x32_bf16 (hi hi + lo hi + hi lo, as for every fp32 product
-// here).  Only v and k are staged (bf16 hi + lo, 70 KB at K = V = 128: two
-// workgroups per CU).  Both products are formed untransposed, D[i][n] (rows
-// i = 16 wv + 4 grp + r, column n = 16 nb + li): the intra-chunk term takes
-// the score accumulator pairs as its A operand and the v^T fragments as its
-// B operand, the one-tile kernel's operands swapped.
+// CU).  Here h is read straight from memory: the output columns are taken in
+// column sets (q, c) holding features 64 q + 4 li + c, so one 16-byte load of
+// h row kappa at columns 64 q + 4 li .. + 3 gives a lane its B-operand value
+// in 4 sets (4 rows x 256 bytes per instruction; the tile's 4 waves share h
+// through L2).  For kappa = 32 a + 8 grp + e, e = 0..7, a set's 8 values are
+// split into bf16 hi + lo in registers and contracted with the q fragments
+// on v_mfma_f32_16x16x32_bf16 (hi hi + lo hi + hi lo, as for every fp32
+// product here).  Only v and k are staged (bf16 hi + lo, 70 KB at K = V =
+// 128: two workgroups per CU); v's columns are stored in set order.  Both
+// products are formed untransposed, D[i][n] (rows i = 16 wv + 4 grp + r):
+// the intra-chunk term takes the score accumulator pairs as its A operand and
+// the v^T fragments of a set as its B operand, so each lane ends with 4
+// consecutive features of a row (one 16-byte store).
 template <int K, int V>
 struct OFCfg {
   static constexpr int kPitch = V + 8;   // v rows (bf16 elements, 16-byte pad)
@@ -381,7 +384,6 @@ struct OFCfg {
   static constexpr int kVLoads = kBT * (V / 4) / kOThreads;  // fp32 16-byte loads per thread
   static constexpr int kKLoads = kBT * (K / 4) / kOThreads;
   static constexpr int KS = K / 32;
-  static constexpr int NB = V / 16;
   static_assert(kBT * (V / 4) % kOThreads == 0 && kBT * (K / 4) % kOThreads == 0, "staging split");
 };
 
@@ -391,7 +393,7 @@ chunk_fwd_o_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
                        const float* __restrict__ g, const float* __restrict__ hs, float* __restrict__ o,
                        float scale, int64_t T, int64_t H, int64_t NT) {
   using C = OFCfg<K, V>;
-  constexpr int KS = C::KS, NB = C::NB;
+  constexpr int KS = C::KS, NQ = V / 64;
   __shared__ __attribute__((aligned(16))) bf16 lv[2 * C::kVTile];  // v hi, v lo
   __shared__ __attribute__((aligned(16))) bf16 lk[2 * C::kKTile];  // k hi, k lo
   __shared__ float gs[kBT];
@@ -431,13 +433,22 @@ chunk_fwd_o_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
   const float gload = (tid < kBT && g) ? g[(tok0 + tid) * H + hh] : 0.f;
 
   // 2. Stage v and k as bf16 hi + lo, and g.
+  // v columns are stored in the order of the output column sets: feature
+  // n = 64 q + 4 m + c at position 64 q + 16 c + m, so the 16 consecutive
+  // positions 64 q + 16 c + li hold the features 64 q + 4 li + c.
 #pragma unroll
   for (int it = 0; it < C::kVLoads; ++it) {
     const int qi = tid + it * kOThreads;
-    const int j = qi / (V / 4), col = (qi - j * (V / 4)) * 4;
+    const int j = qi / (V / 4), m4 = qi - j * (V / 4);
+    const int base = j * C::kPitch + 64 * (m4 >> 4) + (m4 & 15);
     float vals[4];
     unpack16(vr[it], vals, 0.f);
-    lds_put4(vhi + j * C::kPitch + col, vlo + j * C::kPitch + col, vals, true);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const bf16 hi = (bf16)vals[c];
+      vhi[base + 16 * c] = hi;
+      vlo[base + 16 * c] = (bf16)(vals[c] - (float)hi);
+    }
   }
 #pragma unroll
   for (int it = 0; it < C::kKLoads; ++it) {
@@ -452,25 +463,33 @@ chunk_fwd_o_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
   // 3. Inter-chunk term D[i][n] = sum_kappa q[i][kappa] h[kappa][n] (runs
   // while the staging stores drain; h is not in LDS): kappa = 32 a + 8 grp + e
   // in the q fragment's order.
-  const float* hb = hs + (int64_t)blockIdx.x * (K * V) + li;  // h[b, c, hh]: the state of this tile
-  f32x4 acc[NB];
+  // Column set (q, c) holds features n = 64 q + 4 li + c: one 16-byte load per
+  // row gives a lane its 4 column sets' values.
+  const float* hb = hs + (int64_t)blockIdx.x * (K * V) + 4 * li;  // h[b, c, hh]: the state of this tile
+  f32x4 acc[NQ][4];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) acc[nb] = zero4();
+  for (int q4 = 0; q4 < NQ; ++q4)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[q4][c] = zero4();
   bf16x8 qh[KS], ql[KS];
 #pragma unroll
   for (int a = 0; a < KS; ++a) split_bf16x8(qv[a], qh[a], ql[a]);
 #pragma unroll
   for (int a = 0; a < KS; ++a)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      float hv[8];
+    for (int q4 = 0; q4 < NQ; ++q4) {
+      float hv[8][4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) hv[e] = hb[(32 * a + 8 * grp + e) * V + 16 * nb];
-      bf16x8 hh, hl;
-      split_bf16x8(hv, hh, hl);
-      acc[nb] = mfma16x16x32(qh[a], hh, acc[nb]);
-      acc[nb] = mfma16x16x32(ql[a], hh, acc[nb]);
-      acc[nb] = mfma16x16x32(qh[a], hl, acc[nb]);
+      for (int e = 0; e < 8; ++e) unpack16(ldg16(hb + (32 * a + 8 * grp + e) * V + 64 * q4), hv[e], 0.f);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float col[8] = {hv[0][c], hv[1][c], hv[2][c], hv[3][c], hv[4][c], hv[5][c], hv[6][c], hv[7][c]};
+        bf16x8 hh, hl;
+        split_bf16x8(col, hh, hl);
+        acc[q4][c] = mfma16x16x32(qh[a], hh, acc[q4][c]);
+        acc[q4][c] = mfma16x16x32(ql[a], hh, acc[q4][c]);
+        acc[q4][c] = mfma16x16x32(qh[a], hl, acc[q4][c]);
+      }
     }
   lds_barrier();
   // acc[nb][r] holds row i = 16 wv + 4 grp + r: scale it by e^{g_i}.
@@ -478,7 +497,9 @@ chunk_fwd_o_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
   for (int r = 0; r < 4; ++r) {
     const float egi = fast_exp(gs[16 * wv + 4 * grp + r]);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb][r] *= egi;
+    for (int q4 = 0; q4 < NQ; ++q4)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[q4][c][r] *= egi;
   }
 
   // 4. Gated, causally masked scores S^T[j][iq] for key blocks jb <= wv (as
@@ -515,21 +536,25 @@ chunk_fwd_o_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
     split_bf16x8(f, ph, pl);
     const int r0 = tr_row_paired(32 * s2, 0), r1 = tr_row_paired(32 * s2, 1);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const bf16x8 vh = frag_tr(vhi, C::kPitch, r0, r1, 16 * nb);
-      const bf16x8 vl = frag_tr(vlo, C::kPitch, r0, r1, 16 * nb);
-      acc[nb] = mfma16x16x32(ph, vh, acc[nb]);
-      acc[nb] = mfma16x16x32(pl, vh, acc[nb]);
-      acc[nb] = mfma16x16x32(ph, vl, acc[nb]);
-    }
+    for (int q4 = 0; q4 < NQ; ++q4)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const bf16x8 vh = frag_tr(vhi, C::kPitch, r0, r1, 64 * q4 + 16 * c);
+        const bf16x8 vl = frag_tr(vlo, C::kPitch, r0, r1, 64 * q4 + 16 * c);
+        acc[q4][c] = mfma16x16x32(ph, vh, acc[q4][c]);
+        acc[q4][c] = mfma16x16x32(pl, vh, acc[q4][c]);
+        acc[q4][c] = mfma16x16x32(ph, vl, acc[q4][c]);
+      }
   }
 
-  // 6. o[i][16 nb + li] for i = 16 wv + 4 grp + r: 16 lanes cover 64 contiguous bytes of a row.
+  // 6. o[i][64 q + 4 li .. + 3] for i = 16 wv + 4 grp + r: one 16-byte store
+  // per lane, 16 lanes cover 256 contiguous bytes of a row.
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float* orow = o + ((tok0 + 16 * wv + 4 * grp + r) * H + hh) * V + li;
+    float* orow = o + ((tok0 + 16 * wv + 4 * grp + r) * H + hh) * V + 4 * li;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) orow[16 * nb] = acc[nb][r] * scale;
+    for (int q4 = 0; q4 < NQ; ++q4)
+      store4(orow + 64 * q4, f32x4{acc[q4][0][r], acc[q4][1][r], acc[q4][2][r], acc[q4][3][r]} * scale);
   }
 }
 
