@@ -1,0 +1,150 @@
+"""Parity with a visible inter-chunk carry, on the kernels the large grids run.
+
+The configs' logsigmoid gate makes e^{g_last} ~ 1e-20, so the state carried
+from one chunk to the next never changes an asserted value.  These tests use
+the reference's own chunk_fwd_h gate, g = chunk-local cumsum of
+(-0.05 U - 0.005) (kernels/chunk_fwd_h/reference.py:39-45; e^{g_last} ~ 0.15),
+a nonzero initial state and T >= 1024 (16+ chunks), on grids of at least 256
+workgroups (B * H * V / 64), which is where chunk_fwd_h runs its DMA pipeline
+kernel (the config-4 path).  Each test first shows on the CPU that the carry
+matters: the float64 oracle with the carry dropped (or its decay applied
+twice) lies outside the tolerance for every chunk after the first; then it
+checks the GPU against the exact oracle.  Tolerance rtol = atol = 1e-2 (bf16).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import deltanet as odn
+from tests.helpers import assert_close, assert_differs, h_delta_carry_mutant, tokens_chunk_reset
+from theorem_amd import chain, configs
+from theorem_amd.kernels import chunk_fwd_h
+
+pytestmark = pytest.mark.gpu
+
+KV = [(64, 64), (64, 128), (128, 64), (128, 128)]
+TOL = 1e-2
+
+
+def np_(t):
+    return None if t is None else t.detach().double().cpu().numpy()
+
+
+def _grid(V):
+    """(B, H) with B * H * V / 64 = 256 workgroups."""
+    return 4, (64 if V == 64 else 32)
+
+
+def _carry_visible_h(h_true, h_mut, what, post: bool):
+    """Every chunk's states after the first (pre-update storage) or all of them
+    (post-update storage) move beyond the tolerance under the planted mistake."""
+    first = 0 if post else 1
+    for c in range(first, h_true.shape[1]):
+        assert_differs(h_mut[:, c], h_true[:, c], TOL, TOL, f"{what} chunk {c}")
+
+
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("form", ["delta", "reference"])
+def test_h_dma_mild_gate_carry(dev, K, V, form):
+    B, H = _grid(V)
+    T = 1024
+    assert B * H * (V // 64) >= 256
+    print(f"[carry] chunk_fwd_h {form} B={B} T={T} H={H} K={K} V={V} mild gate, h0", flush=True)
+    d = configs.make_h_inputs(B, T, H, K, V, seed=61, device=dev, dtype=torch.bfloat16, gate="mild", h0_std=0.1)
+    k, w, u, g, h0 = (np_(d[n]) for n in ("k", "w", "u", "g", "h0"))
+    if form == "delta":
+        eh, evn, eht = odn.chunk_fwd_h_delta(k, w, u, g, h0=h0)
+        for mode in ("dropped", "double_decay"):
+            mh, mvn, mht = h_delta_carry_mutant(k, w, u, g, h0, mode)
+            _carry_visible_h(eh, mh, f"h, carry {mode}", post=False)
+            assert_differs(mvn, evn, TOL, TOL, f"v_new, carry {mode}")
+            assert_differs(mht, eht, TOL, TOL, f"final state, carry {mode}")
+        h, vn, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=d["g"], initial_state=d["h0"],
+                                                   output_final_state=True))
+        torch.cuda.synchronize()
+        assert_close(vn, evn, TOL, TOL, f"v_new K={K} V={V}")
+    else:
+        pre, _, eht = odn.chunk_fwd_h_delta(k, np.zeros_like(w), u, g, h0=h0)
+        eh = np.concatenate([pre[:, 1:], eht[:, None]], axis=1)
+        for mode in ("dropped", "double_decay"):
+            mpre, _, mht = h_delta_carry_mutant(k, None, u, g, h0, mode)
+            mh = np.concatenate([mpre[:, 1:], mht[:, None]], axis=1)
+            _carry_visible_h(eh, mh, f"h (reference form), carry {mode}", post=True)
+        h, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], v=d["u"], g=d["g"], initial_state=d["h0"],
+                                               output_final_state=True))
+        torch.cuda.synchronize()
+    assert_close(h, eh, TOL, TOL, f"h {form} K={K} V={V}")
+    assert_close(ht, eht, TOL, TOL, f"final state {form} K={K} V={V}")
+
+
+@pytest.mark.parametrize("K,V", KV)
+def test_fused_mild_gate_carry(dev, K, V):
+    # The fused h + o kernel (never writes h) on the same kind of inputs, with
+    # q drawn separately: o, v_new and the final state against the oracle; the
+    # carry check is on o, the output that hides the states.
+    B, H = _grid(V)
+    T = 1024
+    print(f"[carry] fused h+o B={B} T={T} H={H} K={K} V={V} mild gate, h0", flush=True)
+    d = configs.make_h_inputs(B, T, H, K, V, seed=62, device=dev, dtype=torch.bfloat16, gate="mild", h0_std=0.1)
+    # u and h0 scaled by 16 (exact in bf16 / fp32): at the generator's scale
+    # the carried part of o stays under the 1e-2 atol at K = V = 128.  v_new =
+    # u - w S cancels, and its bf16 rounding (S enters w S as bf16) grows with
+    # the scale, so v_new and the final state are held to the scale-equivalent
+    # atol 16e-2 (o, the output the carry check is on, to 1e-2).
+    sc = 16
+    d["u"], d["h0"] = sc * d["u"], sc * d["h0"]
+    gen = torch.Generator().manual_seed(63)
+    q = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16).to(dev)
+    scale = K ** -0.5
+    k, w, u, g, h0 = (np_(d[n]) for n in ("k", "w", "u", "g", "h0"))
+    eh, evn, eht = odn.chunk_fwd_h_delta(k, w, u, g, h0=h0)
+    eo = odn.chunk_fwd_o_diff(np_(q), k, evn, g, eh, scale)
+    for mode in ("dropped", "double_decay"):
+        mh, mvn, _ = h_delta_carry_mutant(k, w, u, g, h0, mode)
+        mo = odn.chunk_fwd_o_diff(np_(q), k, mvn, g, mh, scale)
+        for c in range(1, T // 64):
+            sl = slice(64 * c, 64 * c + 64)
+            assert_differs(mo[:, sl], eo[:, sl], TOL, TOL, f"o chunk {c}, carry {mode}")
+    o, vn, ht = chain.chunk_fwd_fused(q, d["k"], d["w"], d["u"], d["g"], scale, d["h0"], True, True)
+    torch.cuda.synchronize()
+    assert_close(o, eo, TOL, TOL, f"fused o K={K} V={V}")
+    assert_close(vn, evn, TOL, sc * TOL, f"fused v_new K={K} V={V}")
+    assert_close(ht, eht, TOL, sc * TOL, f"fused final state K={K} V={V}")
+
+
+def _chain_inputs(B, T, H, K, V, seed):
+    gen = torch.Generator().manual_seed(seed)
+    q = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16)
+    k = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16)
+    v = torch.randn(B, T, H, V, generator=gen).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    a = -0.05 * torch.rand(B, T, H, generator=gen) - 0.005     # chunk_fwd_h/reference.py:39-45
+    return q, k, v, beta, a
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (128, 128)])
+@pytest.mark.parametrize("fused", [True, False])
+def test_chain_mild_gate_carry(dev, K, V, fused):
+    # The driver from q, k, v, beta and the per-token log decay a (g formed on
+    # the GPU), fused (wy_fwd + fused h + o) and unfused (A-builder,
+    # recompute_w_u, the DMA chunk_fwd_h, chunk_fwd_o), against the token-level
+    # gated delta rule on sampled heads over all 1024 tokens.
+    B, H = _grid(V)
+    T = 1024
+    print(f"[carry] chain fused={fused} B={B} T={T} H={H} K={K} V={V} mild gate", flush=True)
+    q, k, v, beta, a = _chain_inputs(B, T, H, K, V, seed=64)
+    scale = K ** -0.5
+    o, ht = chain.chunk_gated_delta_rule_fwd(q.to(dev), k.to(dev), v.to(dev), beta.to(dev), None, scale,
+                                             output_final_state=True, a=a.to(dev), fused=fused)
+    torch.cuda.synchronize()
+    for b, hh in [(0, 0), (B - 1, H - 1), (2, H // 2 + 1)]:
+        sl = lambda t: np_(t[b:b + 1, :, hh:hh + 1])  # noqa: E731
+        eo, eS = odn.gated_delta_rule_tokens(sl(q), sl(k), sl(v), sl(beta), sl(a), scale)
+        mo = tokens_chunk_reset(sl(q), sl(k), sl(v), sl(beta), sl(a), scale)
+        for c in range(1, T // 64):
+            cs = slice(64 * c, 64 * c + 64)
+            assert_differs(mo[:, cs], eo[:, cs], TOL, TOL, f"o chunk {c} (b={b}, head={hh}), carry dropped")
+        assert_close(o[b:b + 1, :, hh:hh + 1], eo, TOL, TOL, f"chain o (b={b}, head={hh}) fused={fused}")
+        assert_close(ht[b:b + 1, hh:hh + 1], eS, TOL, TOL, f"chain final state (b={b}, head={hh}) fused={fused}")
