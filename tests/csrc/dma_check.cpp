@@ -1,0 +1,437 @@
+// Host-side check of the addressing of the two global -> LDS DMA pipelines
+// (the bf16 chunk_fwd_h kernel and the fused h + o kernel), built with g++ and
+// run by tests/test_dma_layout.py.  It evaluates the index functions the
+// kernels call (theorem_amd/csrc/h_layout.h) and the layout constants they
+// use (theorem_amd/csrc/pipe_cfg.h) for every instantiation, and checks:
+//   * LDS layout: every region inside the workgroup's allocation, aligned and
+//     disjoint;
+//   * DMA: each tile's 16-byte slots are written exactly once, from inside the
+//     chunk's token block, and slot P holds the logical (row, chunk) the
+//     readers expect;
+//   * reads: every fragment read lands on the logical elements its contract
+//     names (for ds_read_b64_tr_b16 after the instruction's lane transpose),
+//     stays inside the tile and is free of LDS bank conflicts per pass
+//     (64 banks of 4 bytes; 32 lanes per pass for 8-byte reads, 16 for 16-byte);
+//   * stores: h, v_new and o tiles are covered exactly once, aligned;
+//   * global bounds: every DMA source, L2 prefetch and store of the extreme
+//     (batch, head, chunk) lies inside its tensor, and the per-lane offsets fit
+//     in 32 bits; the workgroup -> (b * H + head, V-tile) map is a bijection;
+//   * wait counts: replaying each wave's issue order, the vmcnt the kernel
+//     waits for at the top of chunk c retires exactly the DMA of chunk c.
+// Exit status 0 and "dma_check: ok" on success; the first failures are printed.
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <set>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "h_layout.h"
+#include "pipe_cfg.h"
+
+using namespace thm;
+
+static int g_fail = 0;
+static long g_checks = 0;
+#define CHECK(cond, ...)                                                     \
+  do {                                                                       \
+    ++g_checks;                                                              \
+    if (!(cond)) {                                                           \
+      if (g_fail++ < 25) {                                                   \
+        std::fprintf(stderr, "FAIL line %d: ", __LINE__);                    \
+        std::fprintf(stderr, __VA_ARGS__);                                   \
+        std::fprintf(stderr, "\n");                                          \
+      }                                                                      \
+    }                                                                        \
+  } while (0)
+
+// --------------------------------------------------------------------------- tiles
+
+// Logical (row, element) held at byte `a` of a tile written by the DMA.
+static std::pair<int, int> decode(uint32_t a, int rb) {
+  const int P = (int)(a / 16);
+  return {hl::dma_row(P, rb), hl::dma_chunk(P, rb) * 8 + (int)(a % 16) / 2};
+}
+
+// The DMA of one [64 x rb] tile by `waves` waves of `n` 1 KiB instructions:
+// lane `lane` of instruction i of wave w writes LDS slot (w n + i) 64 + lane
+// from dma_src_off of that slot.
+static void check_tile_dma(int rb, int waves, int n, int64_t ts, const char* what) {
+  const int slots = 64 * rb / 16;
+  CHECK(waves * n * 64 == slots, "%s: %d waves x %d DMA instructions do not cover %d slots", what, waves, n, slots);
+  std::vector<int> seen(64 * (rb / 16), 0);
+  for (int w = 0; w < waves; ++w)
+    for (int i = 0; i < n; ++i)
+      for (int lane = 0; lane < 64; ++lane) {
+        const int P = (w * n + i) * 64 + lane;
+        const uint32_t lds = (uint32_t)(w * n * 1024 + i * 1024 + 16 * lane);  // the kernel's M0 base + 16 lane
+        CHECK(lds == (uint32_t)P * 16 && P < slots, "%s: slot %d written at LDS %u", what, P, lds);
+        const uint32_t src = hl::dma_src_off(P, rb, ts);
+        const int64_t row = src / ts, byte = src % ts;
+        CHECK(row >= 0 && row < 64 && byte % 16 == 0 && byte + 16 <= rb,
+              "%s: slot %d source row %lld byte %lld outside the token rows", what, P, (long long)row, (long long)byte);
+        if (row < 0 || row >= 64 || byte + 16 > rb) continue;
+        CHECK(row == hl::dma_row(P, rb) && byte / 16 == hl::dma_chunk(P, rb),
+              "%s: slot %d fetched (%lld, %lld), expected (%d, %d)", what, P, (long long)row, (long long)byte / 16,
+              hl::dma_row(P, rb), hl::dma_chunk(P, rb));
+        seen[row * (rb / 16) + byte / 16]++;
+      }
+  for (size_t q = 0; q < seen.size(); ++q)
+    CHECK(seen[q] == 1, "%s: logical chunk %zu of the tile fetched %d times", what, q, seen[q]);
+  // Every logical element the readers address through tile_off sits where the DMA put it.
+  for (int r = 0; r < 64; ++r)
+    for (int e = 0; e < rb / 2; ++e) {
+      const uint32_t a = hl::tile_off(r, e, rb);
+      CHECK(a + 2 <= (uint32_t)(64 * rb), "%s: tile_off(%d, %d) = %u past the tile", what, r, e, a);
+      const auto d = decode(a, rb);
+      CHECK(d.first == r && d.second == e, "%s: tile_off(%d, %d) holds (%d, %d)", what, r, e, d.first, d.second);
+    }
+}
+
+enum ReadKind { kTr16, kPair, kRow8 };
+
+// Bank-conflict check of one instruction: `addr[lane]`, `bytes` per lane.
+static void check_banks(const uint32_t* addr, int bytes, const char* what, int r0, int c0) {
+  const int per_pass = 256 / bytes;
+  for (int p = 0; p < 64 / per_pass; ++p) {
+    std::set<uint32_t> banks;
+    for (int l = p * per_pass; l < (p + 1) * per_pass; ++l)
+      for (int d = 0; d < bytes / 4; ++d) banks.insert((addr[l] / 4 + d) % 64);
+    CHECK((int)banks.size() == 64, "%s (r0 %d, c0 %d): pass %d hits %zu of 64 banks", what, r0, c0, p, banks.size());
+  }
+}
+
+// One fragment read at block (r0, c0) of a [64 x rb] tile.
+static void check_read(ReadKind kind, int r0, int c0, int rb, const char* what) {
+  uint32_t addr[64];
+  const int bytes = kind == kRow8 ? 16 : 8;
+  for (int lane = 0; lane < 64; ++lane) {
+    const int grp = lane >> 4, li = lane & 15;
+    int row, e;
+    uint32_t a;
+    if (kind == kTr16) {
+      a = hl::tr_frag_off(r0, c0, lane, rb);
+      row = r0 + 4 * grp + li / 4;
+      e = c0 + 4 * (li % 4);
+    } else if (kind == kPair) {
+      a = hl::pair_frag_off(r0, c0, lane, rb);
+      row = r0 + li;
+      e = c0 + 4 * grp;
+    } else {
+      a = hl::row8_frag_off(r0, c0, lane, rb);
+      row = r0 + li;
+      e = c0 + 8 * grp;
+    }
+    addr[lane] = a;
+    CHECK(a % bytes == 0 && a + bytes <= (uint32_t)(64 * rb), "%s: lane %d reads %d bytes at %u", what, lane, bytes, a);
+    for (int i = 0; i < bytes / 2; ++i) {
+      const auto d = decode(a + 2 * i, rb);
+      CHECK(d.first == row && d.second == e + i, "%s (r0 %d, c0 %d): lane %d element %d holds (%d, %d), wants (%d, %d)",
+            what, r0, c0, lane, i, d.first, d.second, row, e + i);
+    }
+  }
+  if (kind == kTr16) {
+    // ds_read_b64_tr_b16: output lane j of a 16-lane group gets, as element r,
+    // element j % 4 of the 8 bytes of source lane 4 r + j / 4.  The consumers
+    // need rows r0 + 4 grp + r of column c0 + j.
+    for (int lane = 0; lane < 64; ++lane) {
+      const int grp = lane >> 4, j = lane & 15;
+      for (int r = 0; r < 4; ++r) {
+        const int src = 16 * grp + 4 * r + j / 4;
+        const auto d = decode(addr[src] + 2 * (j % 4), rb);
+        CHECK(d.first == r0 + 4 * grp + r && d.second == c0 + j, "%s: transposed lane %d element %d holds (%d, %d)",
+              what, lane, r, d.first, d.second);
+      }
+    }
+  }
+  check_banks(addr, bytes, what, r0, c0);
+}
+
+// Every 16-row block position a kernel uses for this read kind and tile.
+static void check_reads(ReadKind kind, int rb, int c_step, const char* what) {
+  for (int r0 = 0; r0 < 64; r0 += 16)
+    for (int c0 = 0; c0 + (kind == kRow8 ? 32 : 16) <= rb / 2; c0 += c_step) check_read(kind, r0, c0, rb, what);
+}
+
+// --------------------------------------------------------------------------- stores
+
+struct Cover {
+  int rows, cols;
+  std::vector<int> n;
+  Cover(int r, int c) : rows(r), cols(c), n((size_t)r * c, 0) {}
+  void add(int r, int c, const char* what) {
+    if (r < 0 || r >= rows || c < 0 || c >= cols) {
+      CHECK(false, "%s: element (%d, %d) outside [%d x %d]", what, r, c, rows, cols);
+      return;
+    }
+    n[(size_t)r * cols + c]++;
+  }
+  void exactly_once(const char* what) const {
+    int bad = 0;
+    for (int x : n) bad += x != 1;
+    CHECK(bad == 0, "%s: %d of %d elements not written exactly once", what, bad, rows * cols);
+  }
+};
+
+// A 16 x 16 tile at (r0, c0) stored with 4 elements per lane at `off(lane)`
+// bytes past the array's origin (rows row_stride bytes apart, eb per element).
+template <typename F>
+static void store_tile(Cover& cv, F off, int64_t row_stride, int eb, const char* what) {
+  for (int lane = 0; lane < 64; ++lane) {
+    const uint64_t a = off(lane);
+    CHECK(a % (4 * eb) == 0, "%s: lane %d store at %llu misaligned", what, lane, (unsigned long long)a);
+    const int row = (int)(a / row_stride);
+    const int c = (int)((a % row_stride) / eb);
+    for (int i = 0; i < 4; ++i) cv.add(row, c + i, what);
+  }
+}
+
+// --------------------------------------------------------------------------- wait counts
+
+// One wave's vector-memory ops in issue order: (is a DMA of chunk `chunk`) or a store (-1).
+struct WaveOps {
+  std::vector<int> ops;
+  void dma(int chunk, int n) { ops.insert(ops.end(), n, chunk); }
+  void other(int n) { ops.insert(ops.end(), n, -1); }
+  // vmcnt(N) retires all but the last N ops: it must retire every DMA op of
+  // `chunk` (safe) and, where `exact`, leave every later op in flight.
+  void check_wait(int chunk, int N, const char* what, int c, bool exact = true) const {
+    int last = -1;
+    for (int i = 0; i < (int)ops.size(); ++i)
+      if (ops[i] == chunk) last = i;
+    CHECK(last >= 0, "%s: chunk %d waited for but never loaded", what, chunk);
+    const int after = (int)ops.size() - 1 - last;
+    CHECK(after >= N, "%s: at chunk %d the wait leaves %d ops in flight, only %d were issued after the chunk's last DMA",
+          what, c, N, after);
+    CHECK(!exact || after == N, "%s: at chunk %d the wait leaves %d ops, %d were issued after the chunk's last DMA",
+          what, c, N, after);
+  }
+};
+
+// --------------------------------------------------------------------------- chunk_fwd_h
+
+struct Shape {
+  int64_t B, T, H;
+};
+static const Shape kShapes[] = {{8, 8192, 16}, {1, 128, 260}, {2, 320, 3}, {4, 1024, 64}, {4, 1024, 32}, {1, 64, 1}};
+
+template <int K, int V, int KS, int NS, bool DELTA, bool HAS_G, bool SV>
+static void check_h() {
+  using C = pipe::PCfg<K, KS, NS, DELTA, HAS_G, SV>;
+  char what[160];
+  std::snprintf(what, sizeof what, "chunk_fwd_h K=%d V=%d KS=%d NS=%d delta=%d g=%d vn=%d", K, V, KS, NS, DELTA, HAS_G,
+                SV);
+  // LDS: per stage [k | w (delta) | u | gates]; then the P1 partials.
+  {
+    std::vector<std::pair<int, int>> reg;
+    for (int s = 0; s < NS; ++s) {
+      const int base = s * C::kStage;
+      reg.push_back({base, base + C::kTileK});
+      if (DELTA) reg.push_back({base + C::kTileK, base + 2 * C::kTileK});
+      const int ub = base + C::kTileK * (DELTA ? 2 : 1);
+      reg.push_back({ub, ub + C::kTileU});
+      if (HAS_G) reg.push_back({ub + C::kTileU, ub + C::kTileU + 64 * 4});
+      CHECK((HAS_G ? ub + C::kTileU + C::kGBytes : ub + C::kTileU) == base + C::kStage, "%s: stage %d size", what, s);
+    }
+    if (C::kXBytes) reg.push_back({NS * C::kStage, NS * C::kStage + C::kXBytes});
+    for (size_t i = 0; i < reg.size(); ++i) {
+      CHECK(reg[i].first % 16 == 0 && reg[i].second <= C::kLds, "%s: LDS region %zu [%d, %d)", what, i, reg[i].first,
+            reg[i].second);
+      for (size_t j = 0; j < i; ++j)
+        CHECK(reg[i].first >= reg[j].second || reg[j].first >= reg[i].second, "%s: LDS regions %zu and %zu overlap", what,
+              i, j);
+    }
+    // P1 partials: wave w, row tile jb, lane: 16 bytes each, read back by wave w ^ 4.
+    if (C::kXBytes)
+      for (int w = 0; w < C::kWaves; ++w)
+        for (int jb = 0; jb < 4; ++jb) {
+          const int hi = ((w * 4 + jb) * 64 + 63) * 16 + 16;
+          CHECK(hi <= C::kXBytes && (w ^ 4) < C::kWaves, "%s: partials slot of wave %d", what, w);
+        }
+  }
+  for (const Shape& sh : kShapes) {
+    const int64_t tsk = sh.H * K * 2, tsv = sh.H * V * 2;
+    // The entry points' 32-bit offset guard.
+    if (64 * sh.H * (K > V ? K : V) * 2 > (INT64_C(1) << 31)) continue;
+    check_tile_dma(C::kRowK, C::kWaves, C::kKDma, tsk, what);
+    check_tile_dma(C::kRowU, C::kWaves, C::kUDma, tsv, what);
+    // Global bounds of the DMA sources for the extreme (b, head, chunk, V-tile).
+    const int64_t NT = sh.T / 64, b = sh.B - 1, hh = sh.H - 1, cc = NT - 1;
+    const int64_t kc0 = ((b * sh.T) * sh.H + hh) * K * 2, kcs = 64 * tsk;
+    const int64_t uc0 = ((b * sh.T) * sh.H + hh) * V * 2 + (V - 64) * 2, ucs = 64 * tsv;
+    uint32_t kmax = 0, umax = 0;
+    for (int P = 0; P < 64 * C::kRowK / 16; ++P) kmax = std::max(kmax, hl::dma_src_off(P, C::kRowK, tsk));
+    for (int P = 0; P < 64 * C::kRowU / 16; ++P) umax = std::max(umax, hl::dma_src_off(P, C::kRowU, tsv));
+    CHECK(kc0 + cc * kcs + kmax + 16 <= sh.B * sh.T * sh.H * K * 2, "%s: k/w DMA past the tensor", what);
+    CHECK(uc0 + cc * ucs + umax + 16 <= sh.B * sh.T * sh.H * V * 2, "%s: u DMA past the tensor", what);
+    const int64_t gc0 = ((b * sh.T) * sh.H + hh) * 4;
+    CHECK(gc0 + cc * 64 * sh.H * 4 + 63 * sh.H * 4 + 4 <= sh.B * sh.T * sh.H * 4, "%s: gate DMA past g", what);
+    // Workgroup -> (b * H + head, V-tile): a bijection.
+    const int64_t BH = sh.B * sh.H;
+    std::vector<int> hit(BH * (V / 64), 0);
+    for (int64_t blk = 0; blk < BH * (V / 64); ++blk) {
+      const hl::BhTile t = hl::xcd_tile(blk, BH, V / 64);
+      if (t.bh < 0 || t.bh >= BH || t.vt < 0 || t.vt >= V / 64) {
+        CHECK(false, "%s: block %lld maps outside the grid", what, (long long)blk);
+        continue;
+      }
+      hit[t.bh * (V / 64) + t.vt]++;
+    }
+    int bad = 0;
+    for (int x : hit) bad += x != 1;
+    CHECK(bad == 0, "%s: B*H=%lld, %d (head, V-tile) pairs not hit exactly once", what, (long long)BH, bad);
+    // Stores: h [K x V] per (b, chunk, head), v_new [64 tokens x V] per chunk.
+    Cover ch(K, V), cv(64, V);
+    for (int vt = 0; vt < V / 64; ++vt) {
+      const int v0 = vt * 64;
+      for (int wi = 0; wi < C::kWaves; ++wi) {
+        const int kh = wi >> 2, wq = wi & 3, kap0 = kh * C::kRows;
+        for (int kb = 0; kb < C::KBH; ++kb)
+          store_tile(ch, [&](int lane) { return hl::rowquad_off(kap0, v0 + 16 * wq, lane, V * 4, 4) + kb * 16 * V * 4; },
+                     V * 4, 4, what);
+        if (DELTA && SV)
+          for (int jj = 0; jj < C::kJbStore; ++jj) {
+            const int tile = C::kJbStore * kh + jj;
+            store_tile(cv, [&](int lane) { return (uint64_t)hl::rowquad_off(0, v0 + 16 * wq, lane, tsv, 2) + 16 * tile * tsv; },
+                       tsv, 2, what);
+          }
+      }
+    }
+    ch.exactly_once(what);
+    if (DELTA && SV) cv.exactly_once(what);
+  }
+  // Wait counts: replay NT chunks.
+  for (int NT = 1; NT <= 5; ++NT)
+    for (int wi = 0; wi < C::kWaves; ++wi) {
+      WaveOps w;
+      const int nd = wi == 0 ? C::kDma0 : C::kDma;
+      // A chunk index past the end is clamped to NT - 1 and loaded again into
+      // a stage no chunk reads: such re-issues are DMAs of no awaited chunk.
+      for (int i = 0; i < NS - 1; ++i) w.dma(i < NT ? i : -2, nd);
+      for (int c = 0; c < NT; ++c) {
+        const int N = wi == 0 ? (c < NS - 1 ? C::kWaitFirst0 : C::kWaitSteady0) : (c < NS - 1 ? C::kWaitFirst : C::kWaitSteady);
+        // The ring-filling chunks 1 .. NS - 2 wait with the first chunk's count,
+        // which is safe but not exact for NS > 2.
+        w.check_wait(c, N, what, c, c == 0 || c >= NS - 1);
+        const int cn = c + NS - 1;
+        w.dma(cn < NT ? cn : -2, nd);
+        w.other(C::kStores);
+      }
+    }
+}
+
+// --------------------------------------------------------------------------- fused
+
+template <int K, int V, bool HAS_G, bool SV>
+static void check_fused() {
+  using C = pipe::FCfg<K, HAS_G, SV>;
+  char what[128];
+  std::snprintf(what, sizeof what, "fused K=%d V=%d g=%d vn=%d", K, V, HAS_G, SV);
+  constexpr int KB2 = C::KB / 2;
+  {
+    std::vector<std::pair<int, int>> reg;
+    for (int s = 0; s < pipe::kFStages; ++s) {
+      const int base = s * C::kStage;
+      for (int m = 0; m < 3; ++m) reg.push_back({base + m * C::kTileK, base + (m + 1) * C::kTileK});
+      reg.push_back({base + 3 * C::kTileK, base + 3 * C::kTileK + C::kTileU});
+      if (HAS_G) reg.push_back({base + 3 * C::kTileK + C::kTileU, base + 3 * C::kTileK + C::kTileU + 256});
+    }
+    const int lp = pipe::kFStages * C::kStage;
+    reg.push_back({lp, lp + C::kPBytes});
+    reg.push_back({lp + C::kPBytes, lp + C::kPBytes + C::kSBytes});
+    reg.push_back({lp + C::kPBytes + C::kSBytes, lp + C::kPBytes + C::kSBytes + C::kVBytes});
+    const int tr = lp + C::kPBytes + C::kSBytes + C::kVBytes;
+    reg.push_back({tr, tr + 256});
+    for (size_t i = 0; i < reg.size(); ++i) {
+      CHECK(reg[i].first % 16 == 0 && reg[i].second <= C::kLds, "%s: LDS region %zu", what, i);
+      for (size_t j = 0; j < i; ++j)
+        CHECK(reg[i].first >= reg[j].second || reg[j].first >= reg[i].second, "%s: LDS regions %zu and %zu overlap", what,
+              i, j);
+    }
+    // Hand-over slots: S pairs (wq, s2 < KB2) and v_new pairs (wq, s2 < 2), 16 bytes per lane.
+    CHECK(((3 * KB2 + KB2 - 1) * 64 + 63) * 16 + 16 <= C::kSBytes, "%s: S hand-over slots", what);
+    CHECK(((3 * 2 + 1) * 64 + 63) * 16 + 16 <= C::kVBytes, "%s: v_new hand-over slots", what);
+  }
+  for (const Shape& sh : kShapes) {
+    if (64 * sh.H * (K > V ? K : V) * 2 > (INT64_C(1) << 31)) continue;
+    const int64_t tsk = sh.H * K * 2, tsv = sh.H * V * 2;
+    check_tile_dma(C::kRowK, 4, C::kKDma, tsk, what);
+    check_tile_dma(C::kRowU, 4, C::kUDma, tsv, what);
+    const int64_t NT = sh.T / 64, b = sh.B - 1, hh = sh.H - 1, cc = NT - 1;
+    const int64_t kc0 = ((b * sh.T) * sh.H + hh) * K * 2;
+    const int64_t uc0 = ((b * sh.T) * sh.H + hh) * V * 2 + (V - 64) * 2;
+    // L2 prefetch lines (4-byte DMAs): k / w / q rows for waves 0-2, u rows
+    // (and the gates) for wave 3.
+    for (int i = 0; i < 4; ++i)
+      for (int lane = 0; lane < 64; ++lane) {
+        const uint32_t ok = hl::l2_line_off(i * 64 + lane, C::kRowK, tsk);
+        CHECK((ok % tsk) + 4 <= (uint32_t)C::kRowK && ok / tsk < 64, "%s: k prefetch line outside the rows", what);
+        CHECK(kc0 + cc * 64 * tsk + ok + 4 <= sh.B * sh.T * sh.H * K * 2, "%s: k prefetch past the tensor", what);
+        const uint32_t ou = hl::l2_line_off((i & 1) * 64 + lane, C::kRowU, tsv);
+        CHECK((ou % tsv) + 4 <= (uint32_t)C::kRowU && ou / tsv < 64, "%s: u prefetch line outside the rows", what);
+        CHECK(uc0 + cc * 64 * tsv + ou + 4 <= sh.B * sh.T * sh.H * V * 2, "%s: u prefetch past the tensor", what);
+      }
+    // Stores of o and v_new: [64 tokens x V] per chunk, quad-transposed lanes.
+    Cover co(64, V);
+    for (int vt = 0; vt < V / 64; ++vt)
+      for (int wq = 0; wq < 4; ++wq)
+        for (int ib = 0; ib < 4; ++ib)
+          store_tile(co, [&](int lane) { return (uint64_t)hl::quadT_off(0, vt * 64 + 16 * wq, lane, tsv, 2) + 16 * ib * tsv; },
+                     tsv, 2, what);
+    co.exactly_once(what);
+  }
+  // Wait counts of the state waves: prologue DMA(0) + prefetch; per chunk the
+  // DMA of c + 1 (4 parts), the prefetch of c + 2, the v_new stores of c.
+  for (int NT = 1; NT <= 5; ++NT)
+    for (int wq = 0; wq < 4; ++wq) {
+      WaveOps w;
+      const int nd = 3 * C::kKDma + C::kUDma + ((HAS_G && wq == 0) ? 1 : 0);
+      w.dma(0, nd);
+      w.other(C::kPf);
+      for (int c = 0; c < NT; ++c) {
+        w.check_wait(c, c < pipe::kFStages - 1 ? C::kWaitFirst : C::kWaitSteady, what, c);
+        w.dma(c + 1 < NT ? c + 1 : -2, nd);
+        w.other(C::kPf);
+        w.other(C::kStores);
+      }
+    }
+}
+
+int main() {
+  // Read patterns of both kernels: k / w / q rows (128 or 256 bytes), the u
+  // V-tile (128 bytes) and the fused kernel's score tile P (128 bytes).
+  for (int rb : {128, 256}) {
+    check_reads(kTr16, rb, 16, "tr16 (k^T, u)");
+    check_reads(kPair, rb, 16, "paired rows (w, q, P)");
+    check_reads(kRow8, rb, 32, "16-byte rows (scores)");
+  }
+#define H_ALL(K, V, NS)                    \
+  check_h<K, V, 2, NS, true, true, true>();   \
+  check_h<K, V, 2, NS, true, true, false>();  \
+  check_h<K, V, 2, NS, true, false, true>();  \
+  check_h<K, V, 2, NS, true, false, false>(); \
+  check_h<K, V, 2, NS, false, true, false>(); \
+  check_h<K, V, 2, NS, false, false, false>();
+  H_ALL(64, 64, pipe::kHStages)
+  H_ALL(64, 128, pipe::kHStages)
+  H_ALL(128, 64, pipe::kHStages)
+  H_ALL(128, 128, pipe::kHStages)
+  H_ALL(128, 128, 3)  // the general ring formulas at another depth
+  check_h<128, 128, 1, 2, true, true, true>();  // the unsplit form
+#define F_ALL(K, V)                   \
+  check_fused<K, V, true, true>();    \
+  check_fused<K, V, true, false>();   \
+  check_fused<K, V, false, true>();   \
+  check_fused<K, V, false, false>();
+  F_ALL(64, 64)
+  F_ALL(64, 128)
+  F_ALL(128, 64)
+  F_ALL(128, 128)
+  if (g_fail) {
+    std::fprintf(stderr, "dma_check: %d of %ld checks failed\n", g_fail, g_checks);
+    return 1;
+  }
+  std::printf("dma_check: ok (%ld checks)\n", g_checks);
+  return 0;
+}

@@ -1,0 +1,93 @@
+"""Host-side check of the DMA pipelines' addressing (CPU).
+
+The bf16 chunk_fwd_h kernel and the fused h + o kernel copy chunk tiles
+global -> LDS with hand-built 32-bit lane offsets, read them back through an
+XOR swizzle and wait for them with hand-counted vmcnt values.  A slip there
+would fault the GPU or race rather than fail a numerical test, so
+tests/csrc/dma_check.cpp evaluates the very index functions and layout
+constants the kernels use (theorem_amd/csrc/h_layout.h, pipe_cfg.h) on the
+host: DMA coverage and global bounds, read/write consistency of the swizzle,
+bank conflicts, store coverage and the wait counts.  The tile-load addressing
+it checks replaces kernels/chunk_fwd_h/kernel.py:103-114 (Triton block
+pointers) and the fused kernel's loads of kernels/chunk_fwd_o/kernel.py:94-136.
+
+The mutation tests plant plausible off-by-one slips in copies of the headers
+and require the checker to fail on each.
+"""
+from __future__ import annotations
+
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+CSRC = ROOT / "theorem_amd" / "csrc"
+SRC = ROOT / "tests" / "csrc" / "dma_check.cpp"
+
+pytestmark = pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+
+
+def _build_and_run(tmp: Path, include_first: Path | None = None) -> subprocess.CompletedProcess:
+    exe = tmp / "dma_check"
+    inc = ([f"-I{include_first}"] if include_first else []) + [f"-I{CSRC}"]
+    subprocess.run(["g++", "-std=c++17", "-O0", "-Wall", *inc, str(SRC), "-o", str(exe)], check=True,
+                   capture_output=True, text=True)
+    return subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+
+
+def test_dma_layout_check_passes(tmp_path):
+    r = _build_and_run(tmp_path)
+    assert r.returncode == 0 and "dma_check: ok" in r.stdout, r.stdout + r.stderr
+
+
+# (header, text in it, planted replacement, what the slip is)
+MUTATIONS = [
+    ("h_layout.h", "return (P % (row_bytes / 16)) ^ swz(P / (row_bytes / 16), row_bytes);",
+     "return ((P + 1) % (row_bytes / 16)) ^ swz(P / (row_bytes / 16), row_bytes);",
+     "dma_chunk: chunk index off by one"),
+    ("h_layout.h", "return (P % (row_bytes / 16)) ^ swz(P / (row_bytes / 16), row_bytes);",
+     "return (P % (row_bytes / 16)) ^ swz(P / (row_bytes / 16) + 1, row_bytes);",
+     "dma_chunk: swizzle of the next row"),
+    ("h_layout.h", "(((e >> 3) ^ swz(r, row_bytes)) << 4)",
+     "(((e >> 3) ^ swz(r + 1, row_bytes)) << 4)",
+     "tile_off: swizzle of the next row"),
+    ("h_layout.h", "+ ((e & 7) << 1));",
+     "+ (((e + 1) & 7) << 1));",
+     "tile_off: element off by one within the chunk"),
+    ("h_layout.h", "(((r & 7) << 1) | ((r >> 3) & 1))",
+     "(((r & 7) << 1) | ((r >> 2) & 1))",
+     "swz: wrong row bit (bank conflicts)"),
+    ("h_layout.h", "return tile_off(r0 + 4 * (lane >> 4) + ((lane & 15) >> 2), c0 + 4 * (lane & 3), row_bytes);",
+     "return tile_off(r0 + 4 * (lane >> 4) + ((lane & 15) >> 2), c0 + 4 * ((lane + 1) & 3), row_bytes);",
+     "tr_frag_off: column group of the neighbouring lane"),
+    ("h_layout.h", "return (uint32_t)(dma_row(P, row_bytes) * tok_stride + dma_chunk(P, row_bytes) * 16);",
+     "return (uint32_t)((dma_row(P, row_bytes) + 1) * tok_stride + dma_chunk(P, row_bytes) * 16);",
+     "dma_src_off: next token row"),
+    ("h_layout.h", "(c0 + 4 * (lane & 3)) * eb);",
+     "(c0 + 4 * (lane & 3) + 1) * eb);",
+     "rowquad_off: store column off by one"),
+    ("h_layout.h", "return {(slot / nvt) * 8 + xcd, slot % nvt};",
+     "return {(slot / nvt) * 8, slot % nvt};",
+     "xcd_tile: XCD index dropped"),
+    ("pipe_cfg.h", "static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma;",
+     "static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma + 1;",
+     "chunk_fwd_h: steady-state wait one op too loose"),
+    ("pipe_cfg.h", "static constexpr int kWaitSteady = kPf + kStores;",
+     "static constexpr int kWaitSteady = kPf + kStores - 1;",
+     "fused: steady-state wait one op too tight"),
+]
+
+
+@pytest.mark.parametrize("header,old,new,what", MUTATIONS, ids=[m[3] for m in MUTATIONS])
+def test_dma_layout_check_catches_planted_slip(tmp_path, header, old, new, what):
+    text = (CSRC / header).read_text()
+    assert text.count(old) == 1, f"mutation site not found in {header}: {old}"
+    mut = tmp_path / "mut"
+    mut.mkdir()
+    for h in ("h_layout.h", "pipe_cfg.h"):
+        (mut / h).write_text((CSRC / h).read_text())
+    (mut / header).write_text(text.replace(old, new))
+    r = _build_and_run(tmp_path, include_first=mut)
+    assert r.returncode != 0, f"planted slip not caught ({what}):\n{r.stdout}{r.stderr}"

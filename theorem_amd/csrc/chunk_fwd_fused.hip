@@ -41,45 +41,18 @@
 // hit that XCD's L2.
 #include "h_layout.h"
 #include "mfma.h"
+#include "pipe_cfg.h"
 #include "vmem.h"
 
 namespace thm {
 namespace {
 
-constexpr int kBT = 64;
-constexpr int kFBV = 64;        // V-tile width
-constexpr int kFThreads = 512;  // 4 state + 4 output wavefronts
-constexpr int kFStages = 2;
-constexpr bool kFPrefetch = true;  // L2 prefetch of the chunk after the one in flight
-
-template <int K, bool HAS_G, bool STORE_VN>
-struct FCfg {
-  static constexpr int kRowK = K * 2;             // bytes per k / w / q row
-  static constexpr int kTileK = kBT * kRowK;
-  static constexpr int kRowU = kFBV * 2;          // bytes per u row of the V-tile
-  static constexpr int kTileU = kBT * kRowU;
-  static constexpr int kGBytes = 1024;            // the chunk's 64 gates, padded to 1 KiB
-  static constexpr int kStage = 3 * kTileK + kTileU + (HAS_G ? kGBytes : 0);
-  static constexpr int KB = K / 16;               // 16-row state tiles per column group
-  static constexpr int kPBytes = kBT * kBT * 2;   // the chunk's scores P, bf16
-  static constexpr int kSBytes = 4 * (KB / 2) * 64 * 16;  // S handed over as bf16 B-operand pairs
-  static constexpr int kVBytes = 4 * 2 * 64 * 16;         // v_new handed over the same way
-  static constexpr int kTrash = 256;                      // landing slot of the L2 prefetch DMAs
-  static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes + kTrash;
-  static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per state wave per k / w / q tile
-  static constexpr int kUDma = kTileU / 1024 / 4;
-  static constexpr int kDma = 3 * kKDma + kUDma + (HAS_G ? 1 : 0);
-  static constexpr int kStores = STORE_VN ? 4 : 0;  // v_new row tiles per state wave
-  static constexpr int kPf = kFPrefetch ? 4 : 0;    // L2 prefetch DMAs per state wave per chunk
-  // Ops a state wave issues after the DMA of chunk c before it waits for it:
-  // the prefetch of chunk c + 1 (and, from c = 1 on, the stores of chunk c - 1).
-  static constexpr int kWaitFirst = kPf;
-  static constexpr int kWaitSteady = kPf + kStores;
-  static_assert(kFStages == 2, "the wait counts assume double buffering");
-  static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
-  static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert(kWaitSteady <= 63, "vmcnt range");
-};
+using pipe::FCfg;
+using pipe::kBT;
+using pipe::kFPrefetch;
+using pipe::kFStages;
+using pipe::kFThreads;
+constexpr int kFBV = pipe::kTileV;  // V-tile width
 
 template <int K, int V, bool HAS_G, bool STORE_VN>
 __global__ void __launch_bounds__(kFThreads)
@@ -93,18 +66,10 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   constexpr int KB2 = C::KB / 2;
   __shared__ __attribute__((aligned(1024))) char lds[C::kLds];
 
-  const int64_t blk = blockIdx.x;
-  int64_t bh, vt;
-  if (BH % 8 == 0) {  // the V-tiles of one (b, head) on one XCD (block i runs on XCD i % 8)
-    const int64_t xcd = blk % 8, slot = blk / 8;
-    bh = (slot / NVT) * 8 + xcd;
-    vt = slot % NVT;
-  } else {
-    bh = blk / NVT;
-    vt = blk % NVT;
-  }
+  const hl::BhTile bt = hl::xcd_tile(blockIdx.x, BH, NVT);
+  const int64_t bh = bt.bh;
   const int64_t b = bh / H, hh = bh % H;
-  const int v0 = (int)vt * kFBV;
+  const int v0 = (int)bt.vt * kFBV;
 
   const int tid = threadIdx.x;
   const int wi = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -136,12 +101,12 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 #pragma unroll
   for (int i = 0; i < C::kKDma; ++i) {
     const int P = (wq * C::kKDma + i) * 64 + lane;
-    koff[i] = (uint32_t)(hl::dma_row(P, C::kRowK) * tsk + hl::dma_chunk(P, C::kRowK) * 16);
+    koff[i] = hl::dma_src_off(P, C::kRowK, tsk);
   }
 #pragma unroll
   for (int i = 0; i < C::kUDma; ++i) {
     const int P = (wq * C::kUDma + i) * 64 + lane;
-    uoff[i] = (uint32_t)(hl::dma_row(P, C::kRowU) * tsv + hl::dma_chunk(P, C::kRowU) * 16);
+    uoff[i] = hl::dma_src_off(P, C::kRowU, tsv);
   }
   const uint32_t goff = (uint32_t)(lane * H * 4);
 
@@ -201,15 +166,12 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   // u rows of the V-tile and the gates; surplus lanes repeat lines.
   uint32_t pfo[4];
   {
-    constexpr int kLinesK = C::kRowK / 64, kLinesU = C::kRowU / 64;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int L = i * 64 + lane;
       if (wq < 3) {
-        pfo[i] = (uint32_t)(((L / kLinesK) % kBT) * tsk + (L % kLinesK) * 64);
+        pfo[i] = hl::l2_line_off(i * 64 + lane, C::kRowK, tsk);
       } else {
-        const int Lu = (i & 1) * 64 + lane;
-        pfo[i] = (HAS_G && i >= 2) ? goff : (uint32_t)(((Lu / kLinesU) % kBT) * tsv + (Lu % kLinesU) * 64);
+        pfo[i] = (HAS_G && i >= 2) ? goff : hl::l2_line_off((i & 1) * 64 + lane, C::kRowU, tsv);
       }
     }
   }
@@ -246,12 +208,10 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   // B = the S pairs sbv, paired contraction order.
   auto rows_times_S = [&](const char* tile, int ib, const bf16x8* sbv) {
     f32x4 acc = zero4();
-    const int row = 16 * ib + li;
 #pragma unroll
     for (int s2 = 0; s2 < KB2; ++s2) {
-      const int e0 = 32 * s2 + 4 * grp;
-      const bf16x4 a0 = *reinterpret_cast<const bf16x4*>(tile + hl::tile_off(row, e0, C::kRowK));
-      const bf16x4 a1 = *reinterpret_cast<const bf16x4*>(tile + hl::tile_off(row, e0 + 16, C::kRowK));
+      const bf16x4 a0 = *reinterpret_cast<const bf16x4*>(tile + hl::pair_frag_off(16 * ib, 32 * s2, lane, C::kRowK));
+      const bf16x4 a1 = *reinterpret_cast<const bf16x4*>(tile + hl::pair_frag_off(16 * ib, 32 * s2 + 16, lane, C::kRowK));
       acc = mfma16x16x32(concat(a0, a1), sbv[s2], acc);
     }
     return acc;
@@ -262,8 +222,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   // row-contiguous layout of vmem.h acc_to_row_quads, which chunk_fwd_h's
   // stores use, is slower here: 366 against 356 us at config 4; the lane
   // transpose lengthens the output waves' path, which bounds this kernel.)
-  const int m4 = li >> 2, qq = li & 3;
-  const uint32_t rowoff0 = (uint32_t)((4 * grp + qq) * tsv + (v0 + 16 * wq + 4 * m4) * 2);
+  const uint32_t rowoff0 = hl::quadT_off(0, v0 + 16 * wq, lane, tsv, 2);
   auto store_rows = [&](bf16* base, int ib, f32x4 val) {
     const f32x4 t = quad_transpose(val);
     bf16x4 ov;
@@ -320,8 +279,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
         issue_part(cnc, cns, jb);
-        const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(
-            tu + hl::tile_off(16 * jb + 4 * grp + (li >> 2), 16 * wq + 4 * (li & 3), C::kRowU)));
+        const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(tu + hl::tr_frag_off(16 * jb, 16 * wq, lane, C::kRowU)));
 #pragma unroll
         for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
         vn[jb] -= rows_times_S(tw, jb, sb);
@@ -356,8 +314,8 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
         f32x4 pt = zero4();
 #pragma unroll
         for (int s2 = 0; s2 < K / 32; ++s2) {
-          const bf16x8 kf = load8(reinterpret_cast<const bf16*>(tk + hl::tile_off(16 * jb + li, 32 * s2 + 8 * grp, C::kRowK)));
-          const bf16x8 qf = load8(reinterpret_cast<const bf16*>(tq + hl::tile_off(16 * ib + li, 32 * s2 + 8 * grp, C::kRowK)));
+          const bf16x8 kf = load8(reinterpret_cast<const bf16*>(tk + hl::row8_frag_off(16 * jb, 32 * s2, lane, C::kRowK)));
+          const bf16x8 qf = load8(reinterpret_cast<const bf16*>(tq + hl::row8_frag_off(16 * ib, 32 * s2, lane, C::kRowK)));
           pt = mfma16x16x32(kf, qf, pt);
         }
         const int i = 16 * ib + li;
@@ -369,7 +327,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
           if constexpr (HAS_G) gate = fast_exp(gs[i] - gs[j]);
           pv[r] = (bf16)((j <= i) ? pt[r] * gate : 0.f);
         }
-        *reinterpret_cast<bf16x4*>(lp + hl::tile_off(i, 16 * jb + 4 * grp, 128)) = pv;
+        *reinterpret_cast<bf16x4*>(lp + hl::pair_frag_off(16 * ib, 16 * jb, lane, 128)) = pv;
       }
     }
     lds_barrier();  // M: P, the S pairs and the v_new pairs of chunk c are in LDS
@@ -401,11 +359,8 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
         if constexpr (HAS_G) S[kb] *= decay;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const int col = 16 * kb + 4 * (li & 3);
-          const bf16x4 a = ds_read_tr16(reinterpret_cast<const bf16*>(
-              tk + hl::tile_off(32 * s2 + 4 * grp + (li >> 2), col, C::kRowK)));
-          const bf16x4 bq = ds_read_tr16(reinterpret_cast<const bf16*>(
-              tk + hl::tile_off(32 * s2 + 16 + 4 * grp + (li >> 2), col, C::kRowK)));
+          const bf16x4 a = ds_read_tr16(reinterpret_cast<const bf16*>(tk + hl::tr_frag_off(32 * s2, 16 * kb, lane, C::kRowK)));
+          const bf16x4 bq = ds_read_tr16(reinterpret_cast<const bf16*>(tk + hl::tr_frag_off(32 * s2 + 16, 16 * kb, lane, C::kRowK)));
           S[kb] = mfma16x16x32(concat(a, bq), vh[s2], S[kb]);
         }
       }
@@ -426,13 +381,12 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
         // Local term: A = P[i][j] rows of lp, B = v_new (pairs), paired order
         // over j; key blocks above the diagonal block contribute zero.
         f32x4 loc = zero4();
-        const int i = 16 * ib + li;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           if (2 * s2 > ib) continue;
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(lp + hl::tile_off(i, 32 * s2 + 4 * grp, 128));
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(lp + hl::pair_frag_off(16 * ib, 32 * s2, lane, 128));
           bf16x4 hi = {};
-          if (2 * s2 + 1 <= ib) hi = *reinterpret_cast<const bf16x4*>(lp + hl::tile_off(i, 32 * s2 + 16 + 4 * grp, 128));
+          if (2 * s2 + 1 <= ib) hi = *reinterpret_cast<const bf16x4*>(lp + hl::pair_frag_off(16 * ib, 32 * s2 + 16, lane, 128));
           loc = mfma16x16x32(concat(lo, hi), vb16[s2], loc);
         }
         store_rows(ob, ib, (acc + loc) * scale);

@@ -18,6 +18,7 @@
 // (theorem_amd/build.py): the bf16 register kernel at config 3 takes 24.4
 // against 25.5 us with them in AGPRs, and the DMA kernel uses no AGPRs either way.
 #include "chunk_fwd_h_reg.h"
+#include "pipe_cfg.h"
 
 namespace thm {
 namespace {
@@ -48,39 +49,8 @@ namespace {
 // issued through vmem.h, so the wait at the top of the loop is an exact count:
 // after this wave's DMA of chunk c it has issued NS - 1 chunks of stores and
 // NS - 2 chunks of DMA.
-template <int K, int KS, int NS, bool DELTA, bool HAS_G, bool STORE_VN>
-struct PCfg {
-  static constexpr int kWaves = 4 * KS;
-  static constexpr int kThreads = 64 * kWaves;
-  static constexpr int kRowK = K * 2;                   // bytes per k / w row
-  static constexpr int kTileK = kBT * kRowK;            // bytes per k / w tile
-  static constexpr int kRowU = kHBV * 2;                // bytes per u row of the V-tile
-  static constexpr int kTileU = kBT * kRowU;
-  static constexpr int kGBytes = 1024;                  // the chunk's 64 gates (wave 0's DMA), padded
-  static constexpr int kStage = kTileK * (DELTA ? 2 : 1) + kTileU + (HAS_G ? kGBytes : 0);
-  static constexpr int kXBytes = (DELTA && KS == 2) ? kWaves * 4 * 64 * 16 : 0;  // P1 partials
-  static constexpr int kLds = NS * kStage + kXBytes;
-  static constexpr int kRows = K / KS;                  // state rows per wave
-  static constexpr int KBH = kRows / 16;                // 16-row accumulator tiles per wave
-  static constexpr int kKDma = kTileK / 1024 / kWaves;  // 1 KiB DMA instructions per wave per k tile
-  static constexpr int kUDma = kTileU / 1024 / kWaves;
-  static constexpr int kJbStore = 4 / KS;               // v_new row tiles stored per wave
-  // DMA instructions per chunk: every wave's share of the k, w, u tiles, plus
-  // the gate load that only wave 0 issues.
-  static constexpr int kDma = kKDma * (DELTA ? 2 : 1) + kUDma;
-  static constexpr int kDma0 = kDma + (HAS_G ? 1 : 0);
-  static constexpr int kStores = KBH + ((DELTA && STORE_VN) ? kJbStore : 0);
-  static constexpr int kWaitFirst = (NS - 2) * kDma;
-  static constexpr int kWaitFirst0 = (NS - 2) * kDma0;
-  static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma;
-  static constexpr int kWaitSteady0 = (NS - 1) * kStores + (NS - 2) * kDma0;
-  static_assert(KS == 1 || KS == 2, "K split");
-  static_assert(NS >= 2, "at least double buffering");
-  static_assert(kKDma >= 1 && kUDma >= 1, "whole DMA instructions per wave");
-  static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
-  static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert(kWaitSteady0 <= 63, "vmcnt range");
-};
+using pipe::PCfg;
+static_assert(pipe::kBT == kBT && pipe::kTileV == kHBV, "one chunk length and V-tile width");
 
 template <int K, int V, int KS, int NS, bool DELTA, bool HAS_G, bool STORE_VN>
 __global__ void __launch_bounds__(256 * KS)
@@ -93,18 +63,10 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
   constexpr int NVT = V / kHBV;
   __shared__ __attribute__((aligned(1024))) char lds[C::kLds];
 
-  const int64_t blk = blockIdx.x;
-  int64_t bh, vt;
-  if (BH % 8 == 0) {  // the V-tiles of one (b, head) on one XCD (block i runs on XCD i % 8)
-    const int64_t xcd = blk % 8, slot = blk / 8;
-    bh = (slot / NVT) * 8 + xcd;
-    vt = slot % NVT;
-  } else {
-    bh = blk / NVT;
-    vt = blk % NVT;
-  }
+  const hl::BhTile bt = hl::xcd_tile(blockIdx.x, BH, NVT);
+  const int64_t bh = bt.bh;
   const int64_t b = bh / H, hh = bh % H;
-  const int v0 = (int)vt * kHBV;
+  const int v0 = (int)bt.vt * kHBV;
 
   const int tid = threadIdx.x;
   const int wi = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -132,12 +94,12 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
 #pragma unroll
   for (int i = 0; i < C::kKDma; ++i) {
     const int P = (wi * C::kKDma + i) * 64 + lane;
-    koff[i] = (uint32_t)(hl::dma_row(P, C::kRowK) * tsk + hl::dma_chunk(P, C::kRowK) * 16);
+    koff[i] = hl::dma_src_off(P, C::kRowK, tsk);
   }
 #pragma unroll
   for (int i = 0; i < C::kUDma; ++i) {
     const int P = (wi * C::kUDma + i) * 64 + lane;
-    uoff[i] = (uint32_t)(hl::dma_row(P, C::kRowU) * tsv + hl::dma_chunk(P, C::kRowU) * 16);
+    uoff[i] = hl::dma_src_off(P, C::kRowU, tsv);
   }
   const uint32_t goff = (uint32_t)(lane * H * 4);
 
@@ -179,11 +141,10 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
   // make the compiler wait for every outstanding operation inside the loop.
   wait_vmcnt<0>();
 
-  // Store offsets after acc_to_row_quads: lane (grp, 4 ra + cb) holds row
-  // 4 grp + ra of a 16-row tile at columns 16 wq + 4 cb .. + 3.
-  const int ra = li >> 2, cb = li & 3;
-  const uint32_t hoff0 = (uint32_t)(((kap0 + 4 * grp + ra) * V + v0 + 16 * wq + 4 * cb) * 4);
-  const uint32_t vnoff0 = (uint32_t)((4 * grp + ra) * tsv + (v0 + 16 * wq + 4 * cb) * 2);
+  // Store offsets of the row-quad layout (acc_to_row_quads) for this wave's
+  // first 16-row tile of h and of v_new; later tiles add 16 rows.
+  const uint32_t hoff0 = hl::rowquad_off(kap0, v0 + 16 * wq, lane, V * 4, 4);
+  const uint32_t vnoff0 = hl::rowquad_off(0, v0 + 16 * wq, lane, tsv, 2);
   // One 16-row tile of h[c] (this wave's rows 16 kb .. 16 kb + 15).  The tiles
   // are stored one at a time inside P2, each next to the MFMAs that update
   // it, instead of as a burst after the chunk's DMA issue: 441 against 483 us
@@ -223,8 +184,7 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
     bf16x4 ur[4];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb)
-      ur[jb] = ds_read_tr16(reinterpret_cast<const bf16*>(
-          tu + hl::tile_off(16 * jb + 4 * grp + (li >> 2), 16 * wq + 4 * (li & 3), C::kRowU)));
+      ur[jb] = ds_read_tr16(reinterpret_cast<const bf16*>(tu + hl::tr_frag_off(16 * jb, 16 * wq, lane, C::kRowU)));
     // w rows 16 jb + li, this wave's K elements, paired order (A operand of P1).
     bf16x4 wa[DELTA ? 4 : 1][C::KBH / 2][2];
     if constexpr (DELTA) {
@@ -233,9 +193,9 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
       for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
         for (int s2 = 0; s2 < C::KBH / 2; ++s2) {
-          const int e0 = kap0 + 32 * s2 + 4 * grp;
-          wa[jb][s2][0] = *reinterpret_cast<const bf16x4*>(tw + hl::tile_off(16 * jb + li, e0, C::kRowK));
-          wa[jb][s2][1] = *reinterpret_cast<const bf16x4*>(tw + hl::tile_off(16 * jb + li, e0 + 16, C::kRowK));
+          const int e0 = kap0 + 32 * s2;
+          wa[jb][s2][0] = *reinterpret_cast<const bf16x4*>(tw + hl::pair_frag_off(16 * jb, e0, lane, C::kRowK));
+          wa[jb][s2][1] = *reinterpret_cast<const bf16x4*>(tw + hl::pair_frag_off(16 * jb, e0 + 16, lane, C::kRowK));
         }
     }
     // k^T fragments of this wave's state rows (A operand of P2), paired order.
@@ -244,11 +204,9 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
     for (int kb = 0; kb < C::KBH; ++kb)
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const int col = kap0 + 16 * kb + 4 * (li & 3);
-        ka[kb][s2][0] = ds_read_tr16(reinterpret_cast<const bf16*>(
-            tk + hl::tile_off(32 * s2 + 4 * grp + (li >> 2), col, C::kRowK)));
-        ka[kb][s2][1] = ds_read_tr16(reinterpret_cast<const bf16*>(
-            tk + hl::tile_off(32 * s2 + 16 + 4 * grp + (li >> 2), col, C::kRowK)));
+        const int col = kap0 + 16 * kb;
+        ka[kb][s2][0] = ds_read_tr16(reinterpret_cast<const bf16*>(tk + hl::tr_frag_off(32 * s2, col, lane, C::kRowK)));
+        ka[kb][s2][1] = ds_read_tr16(reinterpret_cast<const bf16*>(tk + hl::tr_frag_off(32 * s2 + 16, col, lane, C::kRowK)));
       }
     // Gates of this lane's rows j0 = 32 s2 + 4 grp + r and j0 + 16.
     float gl = 0.f;
@@ -364,8 +322,8 @@ chunk_fwd_h_dma_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
 // Measured on MI355X at B=8, T=8192, H=16, K=V=128 (256 workgroups): the K
 // split with a 2-stage ring is the fastest form (3 stages and the unsplit form
 // are slower); every form is bound by HBM traffic, 2.16 GB per launch.
-constexpr int kHKSplit = 2;  // K split of the bf16 pipeline
-constexpr int kHStages = 2;  // DMA ring depth of the bf16 pipeline
+using pipe::kHKSplit;  // K split of the bf16 pipeline
+using pipe::kHStages;  // DMA ring depth of the bf16 pipeline
 
 template <int K, int V, bool DELTA>
 hipError_t launch_h_dma(const void* k, const void* w, const void* vu, const void* g, const void* h0,

@@ -1,0 +1,97 @@
+// Compile-time layout of the two global -> LDS DMA pipelines: the bf16
+// chunk_fwd_h kernel (chunk_fwd_h.hip, PCfg) and the fused h + o kernel
+// (chunk_fwd_fused.hip, FCfg).  Plain constants, shared by the kernels and by
+// the host-side check of their LDS layout, DMA coverage, stores and wait
+// counts (tests/csrc/dma_check.cpp).
+#pragma once
+
+namespace thm {
+namespace pipe {
+
+constexpr int kBT = 64;     // chunk length (tokens)
+constexpr int kTileV = 64;  // state columns per workgroup (V-tile)
+
+// ---------------------------------------------------------------------------
+// chunk_fwd_h, bf16 DMA kernel: 4 KS wavefronts; wave w = 4 kh + wq owns state
+// rows [kh K / KS, (kh + 1) K / KS) and columns 16 wq .. + 15 of the V-tile.
+// Per chunk each wave issues its share of the next chunk's k, w, u DMA (wave 0
+// also the gates), then its v_new and h stores.
+constexpr int kHKSplit = 2;  // K split
+constexpr int kHStages = 2;  // DMA ring depth
+
+template <int K, int KS, int NS, bool DELTA, bool HAS_G, bool STORE_VN>
+struct PCfg {
+  static constexpr int kWaves = 4 * KS;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kRowK = K * 2;                   // bytes per k / w row
+  static constexpr int kTileK = kBT * kRowK;            // bytes per k / w tile
+  static constexpr int kRowU = kTileV * 2;              // bytes per u row of the V-tile
+  static constexpr int kTileU = kBT * kRowU;
+  static constexpr int kGBytes = 1024;                  // the chunk's 64 gates (wave 0's DMA), padded
+  static constexpr int kStage = kTileK * (DELTA ? 2 : 1) + kTileU + (HAS_G ? kGBytes : 0);
+  static constexpr int kXBytes = (DELTA && KS == 2) ? kWaves * 4 * 64 * 16 : 0;  // P1 partials
+  static constexpr int kLds = NS * kStage + kXBytes;
+  static constexpr int kRows = K / KS;                  // state rows per wave
+  static constexpr int KBH = kRows / 16;                // 16-row accumulator tiles per wave
+  static constexpr int kKDma = kTileK / 1024 / kWaves;  // 1 KiB DMA instructions per wave per k tile
+  static constexpr int kUDma = kTileU / 1024 / kWaves;
+  static constexpr int kJbStore = 4 / KS;               // v_new row tiles stored per wave
+  // DMA instructions per chunk: every wave's share of the k, w, u tiles, plus
+  // the gate load that only wave 0 issues.
+  static constexpr int kDma = kKDma * (DELTA ? 2 : 1) + kUDma;
+  static constexpr int kDma0 = kDma + (HAS_G ? 1 : 0);
+  static constexpr int kStores = KBH + ((DELTA && STORE_VN) ? kJbStore : 0);
+  // vmcnt at the top of chunk c: after this wave's DMA of chunk c it has
+  // issued NS - 1 chunks of stores and NS - 2 chunks of DMA.
+  static constexpr int kWaitFirst = (NS - 2) * kDma;
+  static constexpr int kWaitFirst0 = (NS - 2) * kDma0;
+  static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma;
+  static constexpr int kWaitSteady0 = (NS - 1) * kStores + (NS - 2) * kDma0;
+  static_assert(KS == 1 || KS == 2, "K split");
+  static_assert(NS >= 2, "at least double buffering");
+  static_assert(kKDma >= 1 && kUDma >= 1, "whole DMA instructions per wave");
+  static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
+  static_assert(kLds <= 160 * 1024, "LDS budget");
+  static_assert(kWaitSteady0 <= 63, "vmcnt range");
+};
+
+// ---------------------------------------------------------------------------
+// Fused h + o kernel: 8 wavefronts, state waves 0-3 and output waves 4-7, wave
+// wq = w % 4 on columns 16 wq .. + 15 of the V-tile.  The state waves issue the
+// DMA of chunk c + 1 (k, w, q, u and the gates, in four parts), an L2
+// prefetch of chunk c + 2 and their v_new stores of chunk c.
+constexpr int kFThreads = 512;     // 4 state + 4 output wavefronts
+constexpr int kFStages = 2;
+constexpr bool kFPrefetch = true;  // L2 prefetch of the chunk after the one in flight
+
+template <int K, bool HAS_G, bool STORE_VN>
+struct FCfg {
+  static constexpr int kRowK = K * 2;             // bytes per k / w / q row
+  static constexpr int kTileK = kBT * kRowK;
+  static constexpr int kRowU = kTileV * 2;        // bytes per u row of the V-tile
+  static constexpr int kTileU = kBT * kRowU;
+  static constexpr int kGBytes = 1024;            // the chunk's 64 gates, padded to 1 KiB
+  static constexpr int kStage = 3 * kTileK + kTileU + (HAS_G ? kGBytes : 0);
+  static constexpr int KB = K / 16;               // 16-row state tiles per column group
+  static constexpr int kPBytes = kBT * kBT * 2;   // the chunk's scores P, bf16
+  static constexpr int kSBytes = 4 * (KB / 2) * 64 * 16;  // S handed over as bf16 B-operand pairs
+  static constexpr int kVBytes = 4 * 2 * 64 * 16;         // v_new handed over the same way
+  static constexpr int kTrash = 256;                      // landing slot of the L2 prefetch DMAs
+  static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes + kTrash;
+  static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per state wave per k / w / q tile
+  static constexpr int kUDma = kTileU / 1024 / 4;
+  static constexpr int kDma = 3 * kKDma + kUDma + (HAS_G ? 1 : 0);
+  static constexpr int kStores = STORE_VN ? 4 : 0;  // v_new row tiles per state wave
+  static constexpr int kPf = kFPrefetch ? 4 : 0;    // L2 prefetch DMAs per state wave per chunk
+  // Ops a state wave issues after the DMA of chunk c before it waits for it:
+  // the prefetch of chunk c + 1 (and, from c = 1 on, the stores of chunk c - 1).
+  static constexpr int kWaitFirst = kPf;
+  static constexpr int kWaitSteady = kPf + kStores;
+  static_assert(kFStages == 2, "the wait counts assume double buffering");
+  static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
+  static_assert(kLds <= 160 * 1024, "LDS budget");
+  static_assert(kWaitSteady <= 63, "vmcnt range");
+};
+
+}  // namespace pipe
+}  // namespace thm
