@@ -169,4 +169,34 @@ def test_build_A_and_cumsum_validation():
     assert cs(ad=3) == -3 and cs(mode=2) == -6 and cs(bt=128) == -6
     assert cs(g=FAKE + 2) == -5 and cs(a=FAKE + 1, ad=1) == -5
     assert cs(B=1 << 30, T=4096, H=64) == -2  # more (b, chunk, head) lanes than the grid can hold
+    assert cs(B=1 << 16, T=64 * 4096, H=16) == -2  # 2^28 blocks x 256 threads > 2^32 - 1 work-items
+    assert cs(B=1, T=64, H=1 << 62) == -2
     assert cs(B=0) == 0
+
+
+def test_launch_size_limit_is_a_shape_error():
+    """Shapes whose grid x block exceeds HIP's 2^32 - 1 work-items are refused on
+    the host with THM_ERR_BAD_SHAPE (-2), below the entry points' other size
+    limits: 2^24 + 1 tiles of 256 threads, 2^23 + 1 workgroups of 512."""
+    lib = _capi.load_library()
+    tiles = (1 << 24) + 64          # B * T/64 * H with H = 64, B = 1
+    T = 64 * (tiles // 64)
+    wu = lib.thm_recompute_w_u_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, T, 64, 64, 64, 64, 1, 0, None)
+    assert wu == -2
+    o = lib.thm_chunk_fwd_o(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, ctypes.c_float(1.0), 1, T, 64, 64, 64, 64, 1, 0, None)
+    assert o == -2
+    A = lib.thm_wy_build_A(FAKE, FAKE, FAKE, FAKE, 1, T, 64, 64, 64, 1, 1, None)
+    assert A == -2
+    wy = lib.thm_wy_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, T, 64, 64, 64, 64, 1, 1, None)
+    assert wy == -2
+    # (b, head, V-tile) grids of 512-thread workgroups: B * H * V/64 = 2^23 + 2^7.
+    bh = (1 << 22) + 64
+    h = lib.thm_chunk_fwd_h(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, 2, 64, bh // 2, 64, 128, 64, 1,
+                            _capi.THM_H_DELTA, None)
+    assert h == -2
+    f = lib.thm_chunk_gated_delta_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, ctypes.c_float(1.0),
+                                      2, 64, bh // 2, 64, 128, 64, 1, None)
+    assert f == -2
+    # The same entry points accept a shape just inside the limit (their launch is
+    # not reached here: B = 0 returns before it).
+    assert lib.thm_recompute_w_u_fwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, T, 64, 64, 64, 64, 1, 0, None) == 0

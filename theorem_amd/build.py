@@ -87,7 +87,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     OBJ_DIR.mkdir(exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
-    srcs = [CSRC / s for s in SOURCES if (CSRC / s).exists()]
+    missing = [s for s in SOURCES + [FLOORS_SRC] if not (CSRC / s).exists()]
+    if missing:
+        raise RuntimeError(f"missing sources in {CSRC}: {', '.join(missing)}")
+    srcs = [CSRC / s for s in SOURCES]
     objs = [OBJ_DIR / (s.name + ".o") for s in srcs]
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:

@@ -243,6 +243,9 @@ extern "C" int thm_causal_conv1d_fwd(const void* x, const void* weight, const vo
   if (batch > (INT64_C(1) << 40) / dim || batch * dim > (INT64_C(1) << 46) / seqlen)
     return THM_ERR_BAD_SHAPE;
   const int64_t n_rows = batch * dim;
+  // Largest grid: the scalar path's 256-element segments, kConvWaves per block.
+  if (!launch_fits((n_rows * ((seqlen + 255) / 256) + kConvWaves - 1) / kConvWaves, kConvWaves * kWave))
+    return THM_ERR_BAD_SHAPE;
   const int vec = (int)(16 / xe);
   // 16-byte vectors need every row start 16-byte aligned.
   const bool vec_ok = ((uintptr_t)x % 16 == 0) && ((uintptr_t)out % 16 == 0) && (seqlen % vec == 0);

@@ -259,9 +259,8 @@ extern "C" int thm_causal_conv1d_fwd_channels_last(const void* x, const void* we
   const int vec = (int)(16 / xe);
   const bool vec_ok = ((uintptr_t)x % 16 == 0) && ((uintptr_t)out % 16 == 0) && (dim % vec == 0);
   const int64_t groups = vec_ok ? dim / vec : dim;
-  if (batch * ((seqlen + kClSeg - 1) / kClSeg) * ((groups + kClThreads - 1) / kClThreads) >
-      (INT64_C(1) << 31))
-    return THM_ERR_BAD_SHAPE;  // grid x fits 31 bits
+  if (!launch_fits(batch * ((seqlen + kClSeg - 1) / kClSeg) * ((groups + kClThreads - 1) / kClThreads), kClThreads))
+    return THM_ERR_BAD_SHAPE;
   const int wb = (w_dtype == THM_DTYPE_BF16);
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
@@ -293,7 +292,7 @@ extern "C" int thm_causal_conv1d_update(const void* x, void* conv_state, const v
   if (((uintptr_t)x % xe) || ((uintptr_t)out % xe) || ((uintptr_t)conv_state % xe) ||
       ((uintptr_t)weight % we) || (bias && ((uintptr_t)bias % we)))
     return THM_ERR_MISALIGNED;
-  if (batch > (INT64_C(1) << 38) / dim) return THM_ERR_BAD_SHAPE;
+  if (batch > (INT64_C(1) << 38) / dim || !launch_fits((batch * dim + 255) / 256, 256)) return THM_ERR_BAD_SHAPE;
   const int wb = (w_dtype == THM_DTYPE_BF16);
   hipStream_t s = (hipStream_t)stream;
   const hipError_t e =

@@ -448,6 +448,7 @@ extern "C" int thm_chunk_gated_delta_fwd(const void* q, const void* k, const voi
     if (p && ((uintptr_t)p % 4)) return THM_ERR_MISALIGNED;
   if (((uintptr_t)o % 8) || (v_new && ((uintptr_t)v_new % 8))) return THM_ERR_MISALIGNED;
   if (B > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  if (!launch_fits(B * H * (V / kFBV), kFThreads)) return THM_ERR_BAD_SHAPE;
   if (64 * H * (K > V ? K : V) * 2 > (INT64_C(1) << 31)) return THM_ERR_UNSUPPORTED;  // 32-bit lane offsets
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;

@@ -396,6 +396,7 @@ extern "C" int thm_chunk_fwd_h(const void* k, const void* w, const void* vu, con
   for (const void* p : ptrs4)
     if (p && ((uintptr_t)p % 4)) return THM_ERR_MISALIGNED;
   if (B > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  if (!launch_fits(B * H * (V / kHBV), 64 * 4 * kHKSplit)) return THM_ERR_BAD_SHAPE;  // the DMA kernel's block
   // Per-lane offsets within one chunk's token block are 32-bit.
   if (64 * H * (K > V ? K : V) * (kv_dtype == THM_DTYPE_F32 ? 4 : 2) > (INT64_C(1) << 31))
     return THM_ERR_UNSUPPORTED;

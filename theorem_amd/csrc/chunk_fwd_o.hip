@@ -622,6 +622,7 @@ extern "C" int thm_chunk_fwd_o(const void* q, const void* k, const void* v, cons
     if ((uintptr_t)p % 16) return THM_ERR_MISALIGNED;
   if (g && ((uintptr_t)g % 4)) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  if (!launch_fits(B * (T / kBT) * H, kOThreads)) return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = (qkv_dtype == THM_DTYPE_F32)
                      ? dispatch_o<float>(K, V, q, k, v, g, h, o, scale, B, T, H, s)

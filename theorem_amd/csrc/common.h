@@ -73,6 +73,13 @@ __device__ __forceinline__ TileCoord tile_coord(int64_t tile, int64_t H, int64_t
   return {(int64_t)(t - bc * h), (int64_t)b * T + (int64_t)(bc - b * nt) * 64};
 }
 
+// HIP rejects a launch of more than 2^32 - 1 work-items in total.  Every entry
+// point checks its grid against this on the host (with its largest block),
+// so an oversized shape returns THM_ERR_BAD_SHAPE instead of a launch error.
+inline bool launch_fits(int64_t workgroups, int64_t threads) {
+  return workgroups >= 0 && workgroups <= (int64_t)UINT32_MAX / threads;
+}
+
 // Compute units of the current device (queried once per device, then cached;
 // 0 if the query fails).  Used to size persistent grids.
 inline int device_cu_count() {

@@ -106,7 +106,9 @@ extern "C" int thm_chunk_local_cumsum(const void* a, void* g, int64_t B, int64_t
   if (B == 0 || T == 0) return THM_OK;
   if (!a || !g) return THM_ERR_NULL_POINTER;
   if (((uintptr_t)a % (a_dtype == THM_DTYPE_F32 ? 4 : 2)) || ((uintptr_t)g % 4)) return THM_ERR_MISALIGNED;
-  if (B * (T / kBT) * ((H + 15) / 16) > (INT64_C(1) << 31) - 1) return THM_ERR_BAD_SHAPE;  // grid < 2^31
+  const int64_t nbt = B * (T / kBT), hg = (H + kCsHeads - 1) / kCsHeads;  // grid = nbt x hg
+  if (B > (INT64_C(1) << 40) / T || hg > (int64_t)UINT32_MAX / nbt || !launch_fits(nbt * hg, kCsThreads))
+    return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   const bool logsig = mode == THM_GATE_LOGSIGMOID;
   const hipError_t e = (a_dtype == THM_DTYPE_F32) ? launch_cumsum<float>(a, g, B, T, H, logsig, s)

@@ -191,6 +191,7 @@ extern "C" int thm_recompute_w_u_fwd(const void* k, const void* v, const void* b
     if ((uintptr_t)p % 16) return THM_ERR_MISALIGNED;
   if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  if (!launch_fits(B * (T / kBT) * H, kWuThreads)) return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = (kv_dtype == THM_DTYPE_F32)
                      ? dispatch_kv<float>(K, V, k, v, beta, A, g, w, u, B, T, H, s)

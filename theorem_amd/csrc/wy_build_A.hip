@@ -252,6 +252,7 @@ extern "C" int thm_wy_build_A(const void* k, const void* beta, const void* g, vo
   if (((uintptr_t)k % 16) || ((uintptr_t)A % 16)) return THM_ERR_MISALIGNED;
   if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  if (!launch_fits(B * (T / kBT) * H, kABThreads)) return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (k_dtype == THM_DTYPE_F32)

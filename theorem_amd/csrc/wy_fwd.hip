@@ -323,6 +323,7 @@ extern "C" int thm_wy_fwd(const void* k, const void* v, const void* beta, const 
   if (((uintptr_t)w % 8) || ((uintptr_t)u % 8)) return THM_ERR_MISALIGNED;
   if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  if (!launch_fits(B * (T / kBT) * H, kWyThreads)) return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (K == 64 && V == 64) e = launch_wy<64, 64>(k, v, beta, g, w, u, B, T, H, sign, s);
