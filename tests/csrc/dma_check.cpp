@@ -17,7 +17,11 @@
 //     (batch, head, chunk) lies inside its tensor, and the per-lane offsets fit
 //     in 32 bits; the workgroup -> (b * H + head, V-tile) map is a bijection;
 //   * wait counts: replaying each wave's issue order, the vmcnt the kernel
-//     waits for at the top of chunk c retires exactly the DMA of chunk c.
+//     waits for at the top of chunk c retires exactly the DMA of chunk c;
+//   * recompute_w_u's [k | v] tile and chunk_fwd_o's v, h and k tiles
+//     (padded, register-staged): the fragments hold the elements the products
+//     need and are read conflict-free; staging stores are bounded in
+//     conflicts.
 // Exit status 0 and "dma_check: ok" on success; the first failures are printed.
 #include <algorithm>
 #include <cstdint>
@@ -398,6 +402,174 @@ static void check_fused() {
     }
 }
 
+// --------------------------------------------------------------------------- recompute_w_u
+
+// Logical (row, element) at byte `a` of an xtile_off tile.
+static std::pair<int, int> xdecode(uint32_t a, int rb) {
+  const int r = (int)(a / rb), b = (int)(a % rb);
+  return {r, (((b / 16) ^ (hl::xswz(r, rb) << 1)) * 8) + (b % 16) / 2};
+}
+
+// recompute_w_u's [k | v] tile (64 rows of n = K + V bf16 elements, xtile_off):
+// the layout is a bijection, the staging stores (thread q writes elements
+// [col, col + ve) of row q / (n / ve), a wave's stores in 256-byte passes) are
+// conflict-free for 16-byte (bf16 inputs, ve = 8) and 8-byte (fp32 inputs as
+// bf16 hi / lo, ve = 4) stores, and the natural-order ds_read_b64_tr_b16
+// fragments hold the elements the products need, conflict-free.
+static void check_xtile(int n, const char* what) {
+  const int rows = 64, rb = 2 * n;
+  std::vector<int> hit(rows * n, 0);
+  for (int r = 0; r < rows; ++r)
+    for (int e = 0; e < n; ++e) {
+      const uint32_t a = hl::xtile_off(r, e, rb);
+      if (a % 2 || a >= (uint32_t)(rows * rb)) {
+        CHECK(false, "%s: xtile_off(%d, %d) = %u outside the tile", what, r, e, a);
+        continue;
+      }
+      hit[a / 2]++;
+      const auto d = xdecode(a, rb);
+      CHECK(d.first == r && d.second == e, "%s: xtile_off(%d, %d) decodes to (%d, %d)", what, r, e, d.first, d.second);
+    }
+  int bad = 0;
+  for (int x : hit) bad += x != 1;
+  CHECK(bad == 0, "%s: %d tile slots not covered exactly once", what, bad);
+  for (int ve : {8, 4}) {
+    const int cpr = n / ve, bytes = 2 * ve;
+    for (int q0 = 0; q0 < rows * cpr; q0 += 64) {
+      uint32_t addr[64];
+      for (int lane = 0; lane < 64; ++lane) {
+        const int q = q0 + lane, j = q / cpr, col = (q % cpr) * ve;
+        addr[lane] = hl::xtile_off(j, col, rb);
+        CHECK(addr[lane] % bytes == 0, "%s: staging store of row %d col %d misaligned", what, j, col);
+      }
+      check_banks(addr, bytes, what, q0, ve);
+    }
+  }
+  for (int k0 = 0; k0 < rows; k0 += 32)
+    for (int half = 0; half < 2; ++half)
+      for (int c0 = 0; c0 < n; c0 += 16) {
+        uint32_t addr[64];
+        for (int lane = 0; lane < 64; ++lane) {
+          addr[lane] = hl::xtr_frag_off(k0, half, c0, lane, rb);
+          const int grp = lane >> 4, li = lane & 15;
+          for (int i = 0; i < 4; ++i) {
+            const auto d = xdecode(addr[lane] + 2 * i, rb);
+            CHECK(d.first == k0 + 8 * grp + 4 * half + li / 4 && d.second == c0 + 4 * (li % 4) + i,
+                  "%s: fragment lane %d element %d holds (%d, %d)", what, lane, i, d.first, d.second);
+          }
+        }
+        for (int lane = 0; lane < 64; ++lane) {
+          const int grp = lane >> 4, j = lane & 15;
+          for (int r = 0; r < 4; ++r) {
+            const auto d = xdecode(addr[16 * grp + 4 * r + j / 4] + 2 * (j % 4), rb);
+            CHECK(d.first == k0 + 8 * grp + 4 * half + r && d.second == c0 + j,
+                  "%s: transposed lane %d element %d holds (%d, %d)", what, lane, r, d.first, d.second);
+          }
+        }
+        check_banks(addr, 8, what, k0 + 4 * half, c0);
+      }
+}
+
+// Logical (row, element) at byte `a` of a padded tile (rows `pitch` bytes
+// apart; `nat`: rows stored in the nat_row order), or (-1, -1) in the padding.
+static std::pair<int, int> pdecode(uint32_t a, int pitch, int n, bool nat) {
+  const int pr = (int)(a / pitch), b = (int)(a % pitch);
+  if (b >= 2 * n) return {-1, -1};
+  return {nat ? hl::nat_row(pr) : pr, b / 2};
+}
+
+// A padded tile of `rows` rows of `n` bf16 elements, rows `pitch` bytes apart
+// (chunk_fwd_o's h tile: K rows, n = V, natural order; its v tile: 64 rows,
+// n = V, paired order):
+//   * the layout maps the tile one to one into rows * pitch bytes;
+//   * staging stores (thread q writes elements [col, col + ve) of row
+//     q / (n / ve); a wave's stores in 256-byte passes) for each store width
+//     in `ves` (8: 16-byte stores of bf16 inputs; 4: 8-byte stores of 4 values
+//     converted from fp32) are aligned; `max_ways` bounds their conflicts;
+//   * the ds_read_b64_tr_b16 fragments (natural or paired order) hold the
+//     elements the products need, after the lane transpose, conflict-free.
+static void check_padded(int rows, int n, int pitch, bool nat, std::vector<int> ves, int max_ways, const char* what) {
+  std::vector<int> hit((size_t)rows * pitch / 2, 0);
+  for (int r = 0; r < rows; ++r)
+    for (int e = 0; e < n; ++e) {
+      const uint32_t a = nat ? hl::ntile_off(r, e, pitch) : hl::ptile_off(r, e, pitch);
+      if (a % 2 || a >= (uint32_t)(rows * pitch)) {
+        CHECK(false, "%s: element (%d, %d) at %u outside the tile", what, r, e, a);
+        continue;
+      }
+      hit[a / 2]++;
+      const auto d = pdecode(a, pitch, n, nat);
+      CHECK(d.first == r && d.second == e, "%s: element (%d, %d) decodes to (%d, %d)", what, r, e, d.first, d.second);
+    }
+  int bad = 0;
+  for (int x : hit) bad += x > 1;
+  CHECK(bad == 0, "%s: %d slots written twice", what, bad);
+  for (int ve : ves) {
+    const int cpr = n / ve, bytes = 2 * ve;
+    for (int q0 = 0; q0 < rows * cpr; q0 += 64) {
+      uint32_t addr[64];
+      for (int lane = 0; lane < 64; ++lane) {
+        const int q = q0 + lane, j = q / cpr, col = (q % cpr) * ve;
+        addr[lane] = nat ? hl::ntile_off(j, col, pitch) : hl::ptile_off(j, col, pitch);
+        CHECK(addr[lane] % bytes == 0, "%s: staging store of row %d col %d misaligned", what, j, col);
+      }
+      // Worst bank multiplicity per pass.
+      const int per_pass = 256 / bytes;
+      for (int p = 0; p < 64 / per_pass; ++p) {
+        int cnt[64] = {0}, ways = 0;
+        for (int l = p * per_pass; l < (p + 1) * per_pass; ++l)
+          for (int d = 0; d < bytes / 4; ++d) ways = std::max(ways, ++cnt[(addr[l] / 4 + d) % 64]);
+        CHECK(ways <= max_ways, "%s: staging pass %d of q0 %d is %d-way conflicted", what, p, q0, ways);
+      }
+    }
+  }
+  for (int k0 = 0; k0 < rows; k0 += 32)
+    for (int half = 0; half < 2; ++half)
+      for (int c0 = 0; c0 < n; c0 += 16) {
+        uint32_t addr[64];
+        auto base = [&](int grp) { return nat ? k0 + 8 * grp + 4 * half : k0 + 16 * half + 4 * grp; };
+        for (int lane = 0; lane < 64; ++lane) {
+          addr[lane] = nat ? hl::ntr_frag_off(k0, half, c0, lane, pitch) : hl::ptr_frag_off(k0 + 16 * half, c0, lane, pitch);
+          const int grp = lane >> 4, li = lane & 15;
+          for (int i = 0; i < 4; ++i) {
+            const auto d = pdecode(addr[lane] + 2 * i, pitch, n, nat);
+            CHECK(d.first == base(grp) + li / 4 && d.second == c0 + 4 * (li % 4) + i,
+                  "%s: fragment lane %d element %d holds (%d, %d)", what, lane, i, d.first, d.second);
+          }
+        }
+        // After the lane transpose, lane (grp, j) holds rows base + r of column c0 + j.
+        for (int lane = 0; lane < 64; ++lane) {
+          const int grp = lane >> 4, j = lane & 15;
+          for (int r = 0; r < 4; ++r) {
+            const auto d = pdecode(addr[16 * grp + 4 * r + j / 4] + 2 * (j % 4), pitch, n, nat);
+            CHECK(d.first == base(grp) + r && d.second == c0 + j, "%s: transposed lane %d element %d holds (%d, %d)",
+                  what, lane, r, d.first, d.second);
+          }
+        }
+        check_banks(addr, 8, what, k0 + 4 * half, c0);
+      }
+}
+
+// chunk_fwd_o's k tile: 64 rows of K elements at row_pitch, staged by 16-byte
+// stores, read as 16-byte natural-order row fragments (rows r0 + li, elements
+// e0 + 8 grp).
+static void check_row_tile(int n, const char* what) {
+  const int pitch = hl::row_pitch(2 * n);
+  for (int r0 = 0; r0 < 64; r0 += 16)
+    for (int e0 = 0; e0 < n; e0 += 32) {
+      uint32_t addr[64];
+      for (int lane = 0; lane < 64; ++lane) {
+        addr[lane] = hl::prow8_frag_off(r0, e0, lane, pitch);
+        for (int i = 0; i < 8; ++i) {
+          const auto d = pdecode(addr[lane] + 2 * i, pitch, n, false);
+          CHECK(d.first == r0 + (lane & 15) && d.second == e0 + 8 * (lane >> 4) + i, "%s: lane %d element %d", what,
+                lane, i);
+        }
+      }
+      check_banks(addr, 16, what, r0, e0);
+    }
+}
+
 int main() {
   // Read patterns of both kernels: k / w / q rows (128 or 256 bytes), the u
   // V-tile (128 bytes) and the fused kernel's score tile P (128 bytes).
@@ -428,6 +600,21 @@ int main() {
   F_ALL(64, 128)
   F_ALL(128, 64)
   F_ALL(128, 128)
+  for (int K : {64, 128})
+    for (int V : {64, 128}) {
+      char what[96];
+      std::snprintf(what, sizeof what, "recompute_w_u [k | v] tile K=%d V=%d", K, V);
+      check_xtile(K + V, what);
+      std::snprintf(what, sizeof what, "chunk_fwd_o h tile K=%d V=%d", K, V);
+      check_padded(K, V, hl::tr_pitch(2 * V), true, {4}, V == 64 ? 2 : 1, what);
+    }
+  for (int V : {64, 128}) {
+    char what[64];
+    std::snprintf(what, sizeof what, "chunk_fwd_o v tile V=%d", V);
+    check_padded(64, V, hl::tr_pitch(2 * V), false, {8}, V == 64 ? 2 : 1, what);
+    std::snprintf(what, sizeof what, "chunk_fwd_o k tile K=%d", V);
+    check_row_tile(V, what);
+  }
   if (g_fail) {
     std::fprintf(stderr, "dma_check: %d of %ld checks failed\n", g_fail, g_checks);
     return 1;

@@ -11,7 +11,7 @@ bank conflicts, store coverage and the wait counts.  The tile-load addressing
 it checks replaces kernels/chunk_fwd_h/kernel.py:103-114 (Triton block
 pointers) and the fused kernel's loads of kernels/chunk_fwd_o/kernel.py:94-136.
 
-The mutation tests plant plausible off-by-one slips in copies of the headers
+The mutation tests plant plausible slips in copies of the headers
 and require the checker to fail on each.
 """
 from __future__ import annotations
@@ -53,9 +53,12 @@ MUTATIONS = [
     ("h_layout.h", "(((e >> 3) ^ swz(r, row_bytes)) << 4)",
      "(((e >> 3) ^ swz(r + 1, row_bytes)) << 4)",
      "tile_off: swizzle of the next row"),
-    ("h_layout.h", "+ ((e & 7) << 1));",
-     "+ (((e + 1) & 7) << 1));",
+    ("h_layout.h", "return (uint32_t)(r * row_bytes + (((e >> 3) ^ swz(r, row_bytes)) << 4) + ((e & 7) << 1));",
+     "return (uint32_t)(r * row_bytes + (((e >> 3) ^ swz(r, row_bytes)) << 4) + (((e + 1) & 7) << 1));",
      "tile_off: element off by one within the chunk"),
+    ("h_layout.h", "+ (((e >> 3) ^ (xswz(r, row_bytes) << 1)) << 4) + ((e & 7) << 1));",
+     "+ (((e >> 3) ^ (xswz(r, row_bytes) << 1)) << 4) + (((e + 1) & 7) << 1));",
+     "xtile_off: element off by one within the chunk"),
     ("h_layout.h", "(((r & 7) << 1) | ((r >> 3) & 1))",
      "(((r & 7) << 1) | ((r >> 2) & 1))",
      "swz: wrong row bit (bank conflicts)"),
@@ -71,6 +74,21 @@ MUTATIONS = [
     ("h_layout.h", "return {(slot / nvt) * 8 + xcd, slot % nvt};",
      "return {(slot / nvt) * 8, slot % nvt};",
      "xcd_tile: XCD index dropped"),
+    ("h_layout.h", "? ((r & 3) | (((r >> 3) & 1) << 2))",
+     "? ((r & 3) | (((r >> 2) & 1) << 2))",
+     "xswz: wrong row bit (bank conflicts in recompute_w_u)"),
+    ("h_layout.h", ": (((r >> 1) & 1) | (((r >> 3) & 1) << 1));",
+     ": (((r >> 1) & 1) | (((r >> 3) & 1) << 2));",
+     "xswz: a pair pushed past a 384-byte row"),
+    ("h_layout.h", "THM_HD constexpr int tr_pitch(int row_bytes) { return row_bytes + 32; }",
+     "THM_HD constexpr int tr_pitch(int row_bytes) { return row_bytes + 16; }",
+     "tr_pitch: 16-byte pad (bank conflicts in the transposed reads)"),
+    ("h_layout.h", "return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);",
+     "return r;",
+     "nat_row: natural-order rows not permuted (bank conflicts)"),
+    ("h_layout.h", "return (uint32_t)((k0 + 8 * half + nat_row(8 * (lane >> 4) + ((lane & 15) >> 2))) * pitch",
+     "return (uint32_t)((k0 + 4 * half + nat_row(8 * (lane >> 4) + ((lane & 15) >> 2))) * pitch",
+     "ntr_frag_off: half offset not permuted with the rows"),
     ("pipe_cfg.h", "static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma;",
      "static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma + 1;",
      "chunk_fwd_h: steady-state wait one op too loose"),

@@ -26,6 +26,7 @@
 //   4. o[i][n..n+3] = scale * acc.
 #include <type_traits>
 
+#include "h_layout.h"
 #include "mfma.h"
 
 namespace thm {
@@ -34,11 +35,16 @@ namespace {
 constexpr int kBT = 64;
 constexpr int kOThreads = 256;
 
+// LDS tiles of v [64 x V] and h [K x V] (bf16), rows padded by 32 bytes
+// (h_layout.h tr_pitch): v fragments are read in the paired order, h in the
+// natural order with its rows stored in the nat_row order; both are read
+// without bank conflicts at constant offsets.  A 16-byte row pad left ~0.59
+// conflict cycles per access.
 template <int K, int V>
 struct OCfg {
-  static constexpr int kPitch = V + 8;  // LDS row pitch (elements) of the v and h tiles
-  static constexpr int kVTile = kBT * kPitch;
-  static constexpr int kHTile = K * kPitch;
+  static constexpr int kPitchB = hl::tr_pitch(V * 2);  // bytes per v / h row
+  static constexpr int kVTile = kBT * kPitchB / 2;     // bf16 elements
+  static constexpr int kHTile = K * kPitchB / 2;
   static constexpr int kLds = kVTile + kHTile;
   static constexpr int kVCPR = V / 8;                           // 16-byte chunks per v row
   static constexpr int kVLoads = kBT * kVCPR / kOThreads;
@@ -46,6 +52,21 @@ struct OCfg {
   static constexpr int KS = K / 32;                             // contraction steps over K
   static_assert(kBT * kVCPR % kOThreads == 0 && K * (V / 4) % kOThreads == 0, "staging split");
 };
+
+// h^T fragment for contraction step s (rows 32 s .. 32 s + 31, natural order)
+// and output columns 16 nb .. + 15.
+template <int P>
+__device__ __forceinline__ bf16x8 h_frag(const char* tile, int s, int nb, int lane) {
+  return concat(ds_read_tr16(reinterpret_cast<const bf16*>(tile + hl::ntr_frag_off(32 * s, 0, 16 * nb, lane, P))),
+                ds_read_tr16(reinterpret_cast<const bf16*>(tile + hl::ntr_frag_off(32 * s, 1, 16 * nb, lane, P))));
+}
+// v^T fragment for key step s (rows 32 s .. 32 s + 31, paired order) and
+// output columns 16 nb .. + 15.
+template <int P>
+__device__ __forceinline__ bf16x8 v_frag(const char* tile, int s, int nb, int lane) {
+  return concat(ds_read_tr16(reinterpret_cast<const bf16*>(tile + hl::ptr_frag_off(32 * s, 16 * nb, lane, P))),
+                ds_read_tr16(reinterpret_cast<const bf16*>(tile + hl::ptr_frag_off(32 * s + 16, 16 * nb, lane, P))));
+}
 
 template <int K, int V>
 __global__ void __launch_bounds__(kOThreads)
@@ -56,10 +77,11 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
   constexpr int KS = C::KS;
   __shared__ __attribute__((aligned(16))) bf16 lds[C::kLds];
   __shared__ float gs[kBT];
-  bf16* const vhi = lds;
-  bf16* const hhi = lds + C::kVTile;
+  char* const vhi = reinterpret_cast<char*>(lds);
+  char* const hhi = reinterpret_cast<char*>(lds + C::kVTile);
 
-  const TileCoord tc = tile_coord(blockIdx.x, H, NT, T);
+  const int64_t tile = blockIdx.x;
+  const TileCoord tc = tile_coord(tile, H, NT, T);
   const int64_t hh = tc.hh;
   const int64_t tok0 = tc.tok0;
   const int tid = threadIdx.x;
@@ -79,7 +101,7 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
     const int col = (qi - j * C::kVCPR) * 8;
     vr[it] = ldg16_nt(v + ((tok0 + j) * H + hh) * V + col);
   }
-  const float* hsrc = hs + (int64_t)blockIdx.x * (K * V);  // h[b, c, hh]: the state of this tile
+  const float* hsrc = hs + (int64_t)tile * (K * V);  // h[b, c, hh]: the state of this tile
 #pragma unroll
   for (int it = 0; it < C::kHLoads; ++it) {
     const int qi = tid + it * kOThreads;
@@ -106,7 +128,7 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
     const int qi = tid + it * kOThreads;
     const int j = qi / C::kVCPR;
     const int col = (qi - j * C::kVCPR) * 8;
-    *reinterpret_cast<u32x4*>(vhi + j * C::kPitch + col) = vr[it];
+    *reinterpret_cast<u32x4*>(vhi + hl::ptile_off(j, col, C::kPitchB)) = vr[it];
   }
 #pragma unroll
   for (int it = 0; it < C::kHLoads; ++it) {
@@ -115,7 +137,7 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
     const int col = (qi - r * (V / 4)) * 4;
     float vals[4];
     unpack16(hr[it], vals, 0.f);
-    lds_put4(hhi + r * C::kPitch + col, nullptr, vals, false);
+    lds_put4(reinterpret_cast<bf16*>(hhi + hl::ntile_off(r, col, C::kPitchB)), nullptr, vals, false);
   }
   if (tid < kBT) gs[tid] = gload;
   lds_barrier();
@@ -127,11 +149,7 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
   for (int nb = 0; nb < NB; ++nb) {
     acc[nb] = zero4();
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int r0 = tr_row_natural(32 * s, 0), r1 = tr_row_natural(32 * s, 1);
-      const bf16x8 hf = frag_tr(hhi, C::kPitch, r0, r1, 16 * nb);
-      acc[nb] = mfma16x16x32(hf, qh[s], acc[nb]);
-    }
+    for (int s = 0; s < KS; ++s) acc[nb] = mfma16x16x32(h_frag<C::kPitchB>(hhi, s, nb, lane), qh[s], acc[nb]);
   }
   const float gi = gs[i];
   const float egi = fast_exp(gi);
@@ -161,9 +179,8 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
     const float f[8] = {p[2 * s][0], p[2 * s][1], p[2 * s][2], p[2 * s][3],
                         p[2 * s + 1][0], p[2 * s + 1][1], p[2 * s + 1][2], p[2 * s + 1][3]};
     const bf16x8 ph = to_bf16x8(f);
-    const int r0 = tr_row_paired(32 * s, 0), r1 = tr_row_paired(32 * s, 1);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16x16x32(frag_tr(vhi, C::kPitch, r0, r1, 16 * nb), ph, acc[nb]);
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16x16x32(v_frag<C::kPitchB>(vhi, s, nb, lane), ph, acc[nb]);
   }
 
   // 6. o[i][16 nb + 4 grp + 0..3].
@@ -187,11 +204,11 @@ constexpr int kOPipeWGsPerCU = 2;
 
 template <int K, int V>
 struct OPCfg {
-  static constexpr int kPitch = V + 8;   // v, h rows (bf16 elements, 16-byte pad)
-  static constexpr int kKPitch = K + 8;  // k rows
-  static constexpr int kVTile = kBT * kPitch;
-  static constexpr int kHTile = K * kPitch;
-  static constexpr int kKTile = kBT * kKPitch;
+  static constexpr int kPitchB = hl::tr_pitch(V * 2);    // bytes per v / h row (layouts as in OCfg)
+  static constexpr int kKPitchB = hl::row_pitch(K * 2);  // bytes per k row (16-byte row reads)
+  static constexpr int kVTile = kBT * kPitchB / 2;       // bf16 elements
+  static constexpr int kHTile = K * kPitchB / 2;
+  static constexpr int kKTile = kBT * kKPitchB / 2;
   static constexpr int kVLoads = kBT * (V / 8) / kOThreads;  // 16-byte loads per thread
   static constexpr int kHLoads = K * (V / 4) / kOThreads;    // h is fp32
   static constexpr int kKLoads = kBT * (K / 8) / kOThreads;
@@ -221,19 +238,26 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   const int li = lane & 15;
   const int i = 16 * wv + li;  // this lane's query position
 
-  // Tile -> (b, c, head), head fastest (as the one-tile kernel).
-  auto tok_of = [&](int64_t tile, int64_t& hh) {
+  // Tile -> (b, c, head), head fastest (as the one-tile kernel).  The
+  // XCD-aware order of recompute_w_u (h_layout.h xcd_tile_order) would save
+  // ~1.5 % of this kernel's reads (g is the only per-token [B, T, H] array)
+  // but its division pushed this register-bound loop into spills.
+  auto tok_of = [&](int64_t t_, int64_t& hh, int64_t& tile) {
+    tile = t_;
     const TileCoord tc = tile_coord(tile, H, NT, T);
     hh = tc.hh;
     return tc.tok0;
   };
+  char* const lvb = reinterpret_cast<char*>(lv);
+  char* const lhb = reinterpret_cast<char*>(lh);
+  char* const lkb = reinterpret_cast<char*>(lk);
 
   // Prefetched registers of one tile.
   u32x4 vr[C::kVLoads], hr[C::kHLoads], kr[C::kKLoads], qr[KS];
   float gr = 0.f;
-  auto prefetch = [&](int64_t tile) {
-    int64_t hh;
-    const int64_t tok0 = tok_of(tile, hh);
+  auto prefetch = [&](int64_t t_) {
+    int64_t hh, tile;
+    const int64_t tok0 = tok_of(t_, hh, tile);
 #pragma unroll
     for (int it = 0; it < C::kHLoads; ++it) {
       const int qi = tid + it * kOThreads;
@@ -261,7 +285,7 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     for (int it = 0; it < C::kVLoads; ++it) {
       const int qi = tid + it * kOThreads;
       const int j = qi / (V / 8), col = (qi - j * (V / 8)) * 8;
-      *reinterpret_cast<u32x4*>(lv + j * C::kPitch + col) = vr[it];
+      *reinterpret_cast<u32x4*>(lvb + hl::ptile_off(j, col, C::kPitchB)) = vr[it];
     }
 #pragma unroll
     for (int it = 0; it < C::kHLoads; ++it) {
@@ -269,13 +293,13 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       const int r = qi / (V / 4), col = (qi - r * (V / 4)) * 4;
       float vals[4];
       unpack16(hr[it], vals, 0.f);
-      lds_put4(lh + r * C::kPitch + col, nullptr, vals, false);
+      lds_put4(reinterpret_cast<bf16*>(lhb + hl::ntile_off(r, col, C::kPitchB)), nullptr, vals, false);
     }
 #pragma unroll
     for (int it = 0; it < C::kKLoads; ++it) {
       const int qi = tid + it * kOThreads;
       const int j = qi / (K / 8), col = (qi - j * (K / 8)) * 8;
-      *reinterpret_cast<u32x4*>(lk + j * C::kKPitch + col) = kr[it];
+      *reinterpret_cast<u32x4*>(lkb + hl::ptile_off(j, col, C::kKPitchB)) = kr[it];
     }
     if (tid < kBT) gs[tid] = gr;
   };
@@ -292,18 +316,15 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     const int64_t tn = t + gridDim.x;
     if (tn < tiles) prefetch(tn);  // in flight while tile t computes
 
-    int64_t hh;
-    const int64_t tok0 = tok_of(t, hh);
+    int64_t hh, tile;
+    const int64_t tok0 = tok_of(t, hh, tile);
     // Inter-chunk term, scaled by e^{g_i}.
     f32x4 acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       acc[nb] = zero4();
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const bf16x8 hf = frag_tr(lh, C::kPitch, tr_row_natural(32 * s, 0), tr_row_natural(32 * s, 1), 16 * nb);
-        acc[nb] = mfma16x16x32(hf, qh[s], acc[nb]);
-      }
+      for (int s = 0; s < KS; ++s) acc[nb] = mfma16x16x32(h_frag<C::kPitchB>(lhb, s, nb, lane), qh[s], acc[nb]);
     }
     const float gi = gs[i];
     const float egi = fast_exp(gi);
@@ -317,7 +338,8 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       if (jb > wv) continue;  // wave-uniform
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        p[jb] = mfma16x16x32(load8(lk + (16 * jb + li) * C::kKPitch + 32 * s + 8 * grp), qh[s], p[jb]);
+        p[jb] = mfma16x16x32(load8(reinterpret_cast<const bf16*>(lkb + hl::prow8_frag_off(16 * jb, 32 * s, lane, C::kKPitchB))),
+                             qh[s], p[jb]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * jb + 4 * grp + r;
@@ -331,9 +353,8 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       const float f[8] = {p[2 * s][0], p[2 * s][1], p[2 * s][2], p[2 * s][3],
                           p[2 * s + 1][0], p[2 * s + 1][1], p[2 * s + 1][2], p[2 * s + 1][3]};
       const bf16x8 ph = to_bf16x8(f);
-      const int r0 = tr_row_paired(32 * s, 0), r1 = tr_row_paired(32 * s, 1);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16x16x32(frag_tr(lv, C::kPitch, r0, r1, 16 * nb), ph, acc[nb]);
+      for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16x16x32(v_frag<C::kPitchB>(lvb, s, nb, lane), ph, acc[nb]);
     }
     const int64_t orow = (tok0 + i) * H + hh;
 #pragma unroll

@@ -92,6 +92,86 @@ THM_HD constexpr uint32_t quadT_off(int r0, int c0, int lane, int64_t row_stride
   return (uint32_t)((r0 + 4 * (lane >> 4) + (lane & 3)) * row_stride + (c0 + 4 * ((lane & 15) >> 2)) * eb);
 }
 
+// recompute_w_u's [k | v] tile: 64 rows of row_bytes = 2 (K + V) bytes (256,
+// 384 or 512), unpadded, read only as ds_read_b64_tr_b16 fragments in the
+// natural contraction order (rows k0 + 8 grp + 4 half + li / 4, elements
+// c0 + 4 (li % 4)).  A 16-lane quarter reads one aligned 32-byte chunk pair
+// of 4 rows; a 256-byte pass reads the pair at the same logical position in 8
+// rows {r0 .. r0 + 3, r0 + 8 .. r0 + 11}.  Logical pair p of row r sits at
+// p ^ xswz(r), which spreads those 8 rows over the 8 pair positions of a
+// 256-byte bank window: for row_bytes a multiple of 256 xswz takes 8 distinct
+// values over them; for an odd multiple of 128 (384: rows alternating between
+// the two 128-byte halves of the window) it takes 4 per row parity and stays
+// inside aligned groups of 4 pairs, so no row is pushed past its last pair.
+// (Measured at config 4 against the padded layout below: 265 against 269 us,
+// both free of bank conflicts, outputs bit-identical.)
+THM_HD constexpr int xswz(int r, int row_bytes) {
+  return row_bytes % 256 == 0 ? ((r & 3) | (((r >> 3) & 1) << 2)) : (((r >> 1) & 1) | (((r >> 3) & 1) << 1));
+}
+THM_HD constexpr uint32_t xtile_off(int r, int e, int row_bytes) {
+  return (uint32_t)(r * row_bytes + (((e >> 3) ^ (xswz(r, row_bytes) << 1)) << 4) + ((e & 7) << 1));
+}
+// Lane address of the natural-order fragment half `half` at contraction step
+// k0 (a multiple of 32) for output columns c0 .. c0 + 15.
+THM_HD constexpr uint32_t xtr_frag_off(int k0, int half, int c0, int lane, int row_bytes) {
+  return xtile_off(k0 + 8 * (lane >> 4) + 4 * half + ((lane & 15) >> 2), c0 + 4 * (lane & 3), row_bytes);
+}
+
+// chunk_fwd_o's register-staged v, h and k tiles are padded instead of
+// swizzled: a fragment address is then one per-lane base plus a constant,
+// folded into the LDS instruction's offset field, where an XOR swizzle needs
+// a register per fragment (chunk_fwd_o's pipelined kernel, at 252 VGPRs,
+// spilled with it).  Rows are `pitch` bytes apart.
+//   * ds_read_b64_tr_b16 fragments read one aligned 32-byte chunk pair from
+//     each of 8 rows per 256-byte pass.  In the paired contraction order those
+//     are 8 consecutive rows, which land in 8 distinct 32-byte bank groups
+//     when pitch / 32 is odd: tr_pitch.  In the natural order they are rows
+//     r0 .. r0 + 3 and r0 + 8 .. r0 + 11, which no linear pitch separates, so
+//     natural-order tiles store logical row r at physical row nat_row(r) (bits
+//     2 and 3 of r swapped): each pass then reads 8 consecutive physical rows.
+//   * 16-byte row reads (and 8-byte paired-order row reads) take 16 bytes from
+//     each of 16 consecutive rows per pass: conflict-free when pitch / 16 is
+//     odd: row_pitch.
+THM_HD constexpr int tr_pitch(int row_bytes) { return row_bytes + 32; }
+THM_HD constexpr int row_pitch(int row_bytes) { return row_bytes + 16; }
+THM_HD constexpr int nat_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+// Element e of row r: plain (paired-order and row-read tiles) and with the
+// natural-order row permutation.
+THM_HD constexpr uint32_t ptile_off(int r, int e, int pitch) { return (uint32_t)(r * pitch + 2 * e); }
+THM_HD constexpr uint32_t ntile_off(int r, int e, int pitch) { return (uint32_t)(nat_row(r) * pitch + 2 * e); }
+// ds_read_b64_tr_b16 sources of the 16 x 16 block of output columns c0 ..
+// c0 + 15: lane (grp, li) addresses elements c0 + 4 (li % 4) .. + 3 of row
+//   paired order:  r0 + 4 grp + li / 4             (r0 = 32 s + 16 half)
+//   natural order: k0 + 8 grp + 4 half + li / 4    (k0 = 32 s)
+// and output lane j of the group receives rows base .. base + 3 of column c0 + j.
+THM_HD constexpr uint32_t ptr_frag_off(int r0, int c0, int lane, int pitch) {
+  return ptile_off(r0 + 4 * (lane >> 4) + ((lane & 15) >> 2), c0 + 4 * (lane & 3), pitch);
+}
+// (For k0 a multiple of 16, nat_row(k0 + 4 half + x) = k0 + 8 half + nat_row(x)
+// for the lane part x = 8 grp + li / 4: written so, the address is one
+// per-lane base plus a constant.)
+THM_HD constexpr uint32_t ntr_frag_off(int k0, int half, int c0, int lane, int pitch) {
+  return (uint32_t)((k0 + 8 * half + nat_row(8 * (lane >> 4) + ((lane & 15) >> 2))) * pitch + 2 * (c0 + 4 * (lane & 3)));
+}
+// 16-byte natural-order row read: row r0 + li, elements e0 + 8 grp .. + 7.
+THM_HD constexpr uint32_t prow8_frag_off(int r0, int e0, int lane, int pitch) {
+  return ptile_off(r0 + (lane & 15), e0 + 8 * (lane >> 4), pitch);
+}
+
+// XCD-aware order of the tile-parallel kernels' [B, T / 64, H] tile grid.
+// Workgroup i runs on XCD i % 8, each XCD with its own L2.  Launch index t
+// maps to a tile index such that, when the (b, chunk) count BNT is a multiple
+// of 8, the H heads of one (b, chunk) all get launch indices of one residue
+// mod 8 (one XCD): per-token arrays laid out [B, T, H] (beta, g: one cache
+// line holds the values of 16 or 32 heads of a token) are then fetched into
+// one L2 instead of eight.  Otherwise it is the identity.  A bijection of
+// [0, BNT H).
+THM_HD inline uint32_t xcd_tile_order(uint32_t t, int64_t H, int64_t BNT) {
+  if (BNT % 8 != 0) return t;
+  const uint32_t h = (uint32_t)H, slot = t >> 3, sq = slot / h;
+  return (sq * 8u + (t & 7u)) * h + (slot - sq * h);
+}
+
 // Workgroup -> (b * H + head, V-tile) of the recurrence kernels.  Workgroup i
 // runs on XCD i % 8; when B * H is a multiple of 8 the V-tiles of one
 // (b, head) land on one XCD (and its L2), so k, w and q are fetched from HBM
