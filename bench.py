@@ -11,7 +11,8 @@ the kernels are launched on (torch's current stream), averaged over the timed
 steps.  ``roofline`` is for the kernel with the largest share of the step:
 algorithmic bytes per launch / its average duration vs 8 TB/s.  ``traffic``
 is read from profiles/traffic_cfg4.json when that summary of rocprofv3
-FETCH_SIZE / WRITE_SIZE runs exists, else null. ``cpu_baseline`` times the CPU
+FETCH_SIZE / WRITE_SIZE runs exists and was recorded from the kernel sources
+built now (else null, with the reason in ``traffic_note``). ``cpu_baseline`` times the CPU
 oracle on a bounded sample (batch elements of the same workload, as many as
 fit in about 12 s) and scales to a full step. ``floors`` times memory-only
 kernels that move each step kernel's algorithmic bytes in its own tile pattern
@@ -23,8 +24,8 @@ register-only MFMA loop); each kernel's ``mfma_frac_of_measured`` is its flop
 rate against the latter. ``shapes`` gives each kernel's latency at configs
 0-3, the shapes the reference publishes numbers for; ``extensions`` times the
 kernels beyond the four (WY matrix, gate cumsum, channels-last conv, conv
-decode step, fused WY, fused h + o, the whole chunked forward) at config-4
-sizes.
+decode step, fused WY, fused h + o, the whole chunked forward) and the four
+step kernels in fp32, the reference's dtype, at config-4 sizes.
 """
 from __future__ import annotations
 
@@ -73,6 +74,29 @@ def work_o(B, T, H, K, V, eb=2):
     return by, NC * (2 * 64 * 64 * (K + V) + 2 * 64 * K * V)
 
 
+# --------------------------------------------------------------------------- measured traffic
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from profiles/traffic_cfg4.json (two
+    rocprofv3 counter passes, FETCH_SIZE and WRITE_SIZE, calibrated against a
+    plain copy), or None when the summary is missing or was recorded from
+    other kernel sources than the ones built now (theorem_amd.profiling
+    source_digest of the kernel's unit and its headers)."""
+    from theorem_amd.profiling import UNITS, source_digest
+
+    tpath = ROOT / "profiles" / "traffic_cfg4.json"
+    try:
+        rec = json.loads(tpath.read_text()).get(kernel)
+    except (OSError, ValueError):
+        return None, "no counter summary"
+    if not rec:
+        return None, "kernel not in the counter summary"
+    if rec.get("source_digest") != source_digest(UNITS[kernel]):
+        return None, "stale: the kernel's sources changed after the counter run"
+    return rec["hbm_bytes_per_launch"], (f"profiles/traffic_cfg4.json, ratio {rec['ratio']} of the algorithmic "
+                                         f"{rec['algorithmic_bytes']} B")
+
+
 # --------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(torch, inputs, conv_inputs, target_s: float = 12.0):
@@ -87,7 +111,7 @@ def cpu_baseline(torch, inputs, conv_inputs, target_s: float = 12.0):
     from oracle import conv as oconv
     from oracle import deltanet as odn
 
-    n = min(16, len(os.sched_getaffinity(0)))
+    n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
     Bfull = inputs["q"].shape[0]
     x, w, bias = conv_inputs
@@ -122,11 +146,39 @@ def cpu_baseline(torch, inputs, conv_inputs, target_s: float = 12.0):
     conv_s = sorted(t[0] for t in times)[len(times) // 2] / nb
     chain_s = sorted(t[1] for t in times)[len(times) // 2] / nb
     us = (conv_s + chain_s) * Bfull * 1e6
+    # torch-CPU F.conv1d over all the cores, on the same sample (a library
+    # leg beside the single-threaded restatement of scripts/cpu_reference.py).
+    xt = torch.from_numpy(arrs[6])
+    wt = torch.from_numpy(wn).unsqueeze(1)
+    bt = torch.from_numpy(bn)
+    Wd = wn.shape[1]
+
+    def tconv():
+        t0 = time.perf_counter()
+        torch.nn.functional.conv1d(torch.nn.functional.pad(xt, (Wd - 1, 0)), wt, bt, groups=wt.shape[0])
+        return time.perf_counter() - t0
+
+    tconv()
+    tconv_s = sorted(tconv() for _ in range(max(3, reps)))[max(3, reps) // 2] / nb
     return {"value": round(us, 1), "unit": "µs/call", "cores": n, "kind": "port",
             "sample": (f"oracle/ (C conv single-threaded; NumPy fp32 recompute_w_u/chunk_fwd_h/chunk_fwd_o, "
                        f"BLAS threads={n}) on batch elements 0..{nb - 1} of config 4, median of {reps} runs, "
                        f"scaled x{Bfull / nb:g} to the full step; per batch element: conv {1e3 * conv_s:.0f} ms, "
-                       f"chain {1e3 * chain_s:.0f} ms")}
+                       f"chain {1e3 * chain_s:.0f} ms"),
+            "legs_us": {"conv_oracle_c_1_thread": round(conv_s * Bfull * 1e6, 1),
+                        f"conv_torch_cpu_{n}_threads": round(tconv_s * Bfull * 1e6, 1),
+                        f"chain_oracle_numpy_{n}_threads": round(chain_s * Bfull * 1e6, 1)},
+            "host": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 # --------------------------------------------------------------------------- per-shape latency
@@ -142,7 +194,15 @@ def shape_latencies(torch, dev, warmup: int = 5, iters: int = 50, batched: int =
                    event runs after that write, by which time the launch is
                    queued, so this is the kernel on cold caches;
       us_batched   ``batched`` back-to-back calls under one event pair, per call
-                   (bounded below by the host launch rate for tiny kernels)."""
+                   (bounded below by the host launch rate for tiny kernels);
+      us_kernel    median with a spin kernel (torch.cuda._sleep) queued ahead of
+                   the start event: the kernel alone on warm caches;
+      host_us      host wall time per call of ``batched`` back-to-back calls
+                   queued behind a spin kernel: the host side of a call (Python
+                   wrapper, output allocation, ctypes, HIP launch; the launch
+                   alone is ~2.3 us through any HIP launch API on the box).
+    On ROCm the event pair of us_ref does not open before the kernel's own
+    dispatch, so us_ref is close to us_kernel and host_us is the host cost."""
     from theorem_amd import configs
     from theorem_amd.kernels import causal_conv1d, chunk_fwd_h, chunk_fwd_o, recompute_w_u
 
@@ -185,6 +245,10 @@ def shape_latencies(torch, dev, warmup: int = 5, iters: int = 50, batched: int =
             return sorted(ts)
         ref = timed(None)
         cold = timed(flush.zero_)
+        # Kernel alone on warm caches: a spin kernel ahead of the start event
+        # keeps the GPU busy while the host enqueues the call, so the event
+        # pair brackets the kernel only; us_ref - us_kernel is the host side.
+        warm = timed(lambda: torch.cuda._sleep(200000))
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         for _ in range(batched):
@@ -192,7 +256,16 @@ def shape_latencies(torch, dev, warmup: int = 5, iters: int = 50, batched: int =
         e.record()
         torch.cuda.synchronize()
         bat = s.elapsed_time(e) * 1e3 / batched
+        # Host side of a call: wall time per call of back-to-back calls with
+        # the GPU kept busy ahead of them (the launches only queue).
+        torch.cuda._sleep(20000000)
+        t0 = time.perf_counter()
+        for _ in range(batched):
+            fn()
+        host = (time.perf_counter() - t0) * 1e6 / batched
+        torch.cuda.synchronize()
         out[cfg] = {"kernel": name, "shape": shape, "us_ref": round(ref[0], 2),
+                    "us_kernel": round(warm[len(warm) // 2], 2), "host_us": round(host, 2),
                     "us_cold_min": round(cold[0], 2), "us_cold_p50": round(cold[len(cold) // 2], 2),
                     "us_batched": round(bat, 2), "bytes": by, "flops": fl,
                     "hbm_frac_cold_min": round(by / (cold[0] * 1e-6) / HBM_PEAK, 4)}
@@ -307,8 +380,9 @@ def work_build_A(B, T, H, K, eb=2):
 
 def extension_timings(torch, inp, conv_in, iters: int = 10):
     """The kernels beyond the four (WY matrix, gate cumsum, channels-last conv,
-    conv decode step, fused WY, fused h + o, the whole chunked forward) at config-4
-    sizes: HIP events around ``iters`` back-to-back launches after one warm-up."""
+    conv decode step, fused WY, fused h + o, the whole chunked forward) and the
+    four in fp32 (the reference's dtype), at config-4 sizes: HIP events around
+    ``iters`` back-to-back launches after one warm-up."""
     from theorem_amd import chain
     from theorem_amd.kernels import causal_conv1d, recompute_w_u
 
@@ -346,6 +420,28 @@ def extension_timings(torch, inp, conv_in, iters: int = 10):
                                                  output_final_state=True),
         N * (K * 2 + V * 2 + 8) + N * (K * 2 + V * 2) + N * (3 * K * 2 + V * 2 + 4) + N * V * 2 + B * H * K * V * 4,
         "the whole chunked forward from (q, k, v, beta, g): fused WY (A, w, u), fused h + o")
+    # The reference's own dtype (fp32; kernel.py asserts it) at config-4 sizes.
+    from theorem_amd.kernels import chunk_fwd_h, chunk_fwd_o
+    k32, v32, q32 = inp["k"].float(), inp["v"].float(), inp["q"].float()
+    w32, u32 = ww.float(), uu.float()
+    h32 = torch.zeros(B, T // 64, H, K, V, device=k32.device)
+    x32, w32c, b32 = x.float(), w.float(), b.float()
+    g, beta, A, scale = inp["g"], inp["beta"], inp["A"], inp["scale"]
+    cases["fp32_causal_conv1d"] = (lambda: causal_conv1d.custom_kernel((x32, w32c, b32)),
+                                   work_conv(Bc, D, S, w.shape[1], eb=4, ebw=4)[0], f"({Bc},{D},{S},W=4) fp32")
+    cases["fp32_recompute_w_u"] = (
+        lambda: recompute_w_u.custom_kernel(recompute_w_u.Data(k=k32, v=v32, beta=beta, A=A, g=g, B=B, T=T, H=H,
+                                                               K=K, V=V)),
+        work_wu(B, T, H, K, V, eb=4)[0], f"({B},{T},{H},{K},{V}) fp32")
+    cases["fp32_chunk_fwd_h"] = (
+        lambda: chunk_fwd_h.custom_kernel(dict(k=k32, w=w32, u=u32, g=g, output_final_state=True)),
+        work_h(B, T, H, K, V, eb=4)[0], f"({B},{T},{H},{K},{V}) fp32, delta form")
+    cases["fp32_chunk_fwd_h_reference_form"] = (
+        lambda: chunk_fwd_h.custom_kernel(dict(k=k32, v=v32, g=g)),
+        N * (K + V) * 4 + 4 * N + (N // 64) * K * V * 4, f"({B},{T},{H},{K},{V}) fp32, the reference's (k, v, g) -> h")
+    cases["fp32_chunk_fwd_o"] = (
+        lambda: chunk_fwd_o.custom_kernel(dict(q=q32, k=k32, v=v32, g=g, h=h32, scale=scale)),
+        work_o(B, T, H, K, V, eb=4)[0], f"({B},{T},{H},{K},{V}) fp32")
     out = {}
     for name, (fn, by, shape) in cases.items():
         fn()
@@ -481,17 +577,12 @@ def main() -> int:
                       "hbm_frac": round(by / (us * 1e-6) / HBM_PEAK, 4),
                       "mfma_frac": round(fl / (us * 1e-6) / MFMA_BF16_PEAK, 4)}
     dom = max(names, key=lambda n: per[n])
-    traffic = None
-    tpath = ROOT / "profiles" / "traffic_cfg4.json"
-    if tpath.exists() and not args.small:
-        try:
-            traffic = json.loads(tpath.read_text()).get(dom, {}).get("hbm_bytes_per_launch")
-        except Exception:  # noqa: BLE001
-            traffic = None
+    traffic, traffic_note = measured_traffic(dom) if not args.small else (None, "not measured at --small")
     by, _ = works[dom]
     achieved = by / (per[dom] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic}
+                "unit": "GB/s", "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": traffic,
+                "traffic_note": traffic_note}
 
     floors = peaks = None
     if not args.small:

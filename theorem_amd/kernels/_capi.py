@@ -60,6 +60,8 @@ _lock = threading.Lock()
 def load_library(path: Path | str | None = None) -> ctypes.CDLL:
     """Load (once) and type the shared library; raise if it is absent or mismatched."""
     global _lib
+    if path is None and _lib is not None:  # the per-call fast path: no lock once loaded
+        return _lib
     with _lock:
         if _lib is not None and path is None:
             return _lib
@@ -117,6 +119,53 @@ def stream_of(t: torch.Tensor) -> int:
     if _raw_stream is not None:
         return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def dev_ptrs(*ts: torch.Tensor | None) -> tuple[list, list | None]:
+    """Device pointers of the given tensors (None stays None) for the C ABI.
+
+    Every tensor must be on one GPU.  A tensor that is not dense row-major or
+    not 16-byte aligned is copied first (the kernels use fixed 16-byte vector
+    addressing); the copies are returned as the second item, to be kept alive
+    until the launch has been enqueued.  This is the per-call host path of
+    every wrapper, so it uses the cheapest tensor queries (is_cuda,
+    get_device, is_contiguous, data_ptr: ~0.25 us per tensor)."""
+    dev = -1
+    out = []
+    keep = None
+    for t in ts:
+        if t is None:
+            out.append(None)
+            continue
+        if not t.is_cuda:
+            raise AssertionError("all inputs must be on the MI355X device (torch 'cuda')")
+        d = t.get_device()
+        if dev < 0:
+            dev = d
+        elif d != dev:
+            raise AssertionError(f"inputs on different devices: cuda:{dev} and cuda:{d}")
+        if not t.is_contiguous():
+            t = t.contiguous()
+            keep = (keep or []) + [t]
+        p = t.data_ptr()
+        if p & 15:
+            t = t.clone()
+            keep = (keep or []) + [t]
+            p = t.data_ptr()
+        out.append(p)
+    return out, keep
+
+
+_devices: dict = {}
+
+
+def device_of(t: torch.Tensor) -> torch.device:
+    """t's torch.device, from a per-index cache (t.device builds a new object)."""
+    i = t.get_device()
+    d = _devices.get(i)
+    if d is None:
+        d = _devices[i] = t.device
+    return d
 
 
 def require_device(*ts: torch.Tensor | None) -> torch.device:

@@ -37,26 +37,30 @@ def custom_kernel(data):
     B, T, H, K = k.shape
     V = vu.shape[-1]
     for key, val in (("B", B), ("T", T), ("H", H), ("K", K), ("V", V)):
-        assert data.get(key, val) == val, f"data[{key!r}]={data[key]} disagrees with the tensors ({val})"
+        if key in data and data[key] != val:
+            raise AssertionError(f"data[{key!r}]={data[key]} disagrees with the tensors ({val})")
     assert T % CHUNK_SIZE == 0, f"T={T} must be divisible by {CHUNK_SIZE}"
     NT = T // CHUNK_SIZE
-    assert vu.shape[:3] == (B, T, H)
-    assert w is None or w.shape == (B, T, H, K)
-    assert g is None or g.shape == (B, T, H)
-    assert h0 is None or h0.shape == (B, H, K, V)
-    assert k.dtype == vu.dtype and (w is None or w.dtype == k.dtype), "k, v/u, w must share a dtype"
-    _capi.require_device(k, w, vu, g, h0)
-    _capi.require_f32(g, "g")
-    _capi.require_f32(h0, "initial_state")
+    if vu.shape[:3] != (B, T, H) or (w is not None and w.shape != k.shape) or (
+            g is not None and g.shape != (B, T, H)) or (h0 is not None and h0.shape != (B, H, K, V)):
+        raise AssertionError(f"shapes: k {tuple(k.shape)}, v/u {tuple(vu.shape)}, "
+                             f"w {None if w is None else tuple(w.shape)}, g {None if g is None else tuple(g.shape)}, "
+                             f"initial_state {None if h0 is None else tuple(h0.shape)}")
+    if k.dtype is not vu.dtype or (w is not None and w.dtype is not k.dtype):
+        raise AssertionError("k, v/u, w must share a dtype")
+    f32 = torch.float32
+    if (g is not None and g.dtype is not f32) or (h0 is not None and h0.dtype is not f32):
+        raise AssertionError("g and initial_state must be float32")
     code = _capi.dtype_code(k, "k")
-    k, w, vu, g, h0 = (_capi.prep(t, "") for t in (k, w, vu, g, h0))
+    (pk, pw, pu, pg, ph0), keep = _capi.dev_ptrs(k, w, vu, g, h0)
 
-    h = torch.empty(B, NT, H, K, V, device=k.device, dtype=torch.float32)
-    v_new = torch.empty_like(vu) if want_vn else None
-    ht = torch.empty(B, H, K, V, device=k.device, dtype=torch.float32) if want_ht else None
+    dev = _capi.device_of(k)
+    h = torch.empty((B, NT, H, K, V), dtype=f32, device=dev)
+    v_new = (torch.empty_like(vu) if vu.is_contiguous() else vu.new_empty(vu.shape)) if want_vn else None
+    ht = torch.empty((B, H, K, V), dtype=f32, device=dev) if want_ht else None
     status = _capi.load_library().thm_chunk_fwd_h(
-        _capi.ptr(k), _capi.ptr(w), _capi.ptr(vu), _capi.ptr(g), _capi.ptr(h0),
-        _capi.ptr(h), _capi.ptr(v_new), _capi.ptr(ht),
+        pk, pw, pu, pg, ph0, h.data_ptr(), None if v_new is None else v_new.data_ptr(),
+        None if ht is None else ht.data_ptr(),
         B, T, H, K, V, CHUNK_SIZE, code, _capi.THM_H_DELTA if delta else 0, _capi.stream_of(k))
     _capi.check(status, "thm_chunk_fwd_h")
     if delta:

@@ -27,17 +27,19 @@ def custom_kernel(data: Dict[str, Any]) -> torch.Tensor:
     NT = h.shape[1]
     assert T % BT == 0, f"T={T} must be divisible by BT={BT}"
     assert NT == T // BT, f"NT={NT} must equal T/BT={T // BT}"
-    assert k.shape == (B, T, H, K) and v.shape[:3] == (B, T, H) and h.shape == (B, NT, H, K, V)
-    assert g is None or g.shape == (B, T, H)
-    assert q.dtype == k.dtype == v.dtype, "q, k, v must share a dtype"
-    _capi.require_device(q, k, v, g, h)
-    _capi.require_f32(g, "g")
-    _capi.require_f32(h, "h")
+    if k.shape != q.shape or v.shape[:3] != (B, T, H) or h.shape != (B, NT, H, K, V) or (
+            g is not None and g.shape != (B, T, H)):
+        raise AssertionError(f"shapes: q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}, "
+                             f"h {tuple(h.shape)}, g {None if g is None else tuple(g.shape)}")
+    if not (q.dtype is k.dtype is v.dtype):
+        raise AssertionError("q, k, v must share a dtype")
+    if h.dtype is not torch.float32 or (g is not None and g.dtype is not torch.float32):
+        raise AssertionError("g and h must be float32")
     code = _capi.dtype_code(q, "q")
-    q, k, v, g, h = (_capi.prep(t, "") for t in (q, k, v, g, h))
-    o = torch.empty(B, T, H, V, dtype=q.dtype, device=q.device)
+    (pq, pk, pv, pg, ph), keep = _capi.dev_ptrs(q, k, v, g, h)
+    # o has q's dtype (kernel.py:183), which v shares, and v's shape.
+    o = torch.empty_like(v) if v.is_contiguous() else v.new_empty(v.shape)
     status = _capi.load_library().thm_chunk_fwd_o(
-        _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(g), _capi.ptr(h), _capi.ptr(o), scale,
-        B, T, H, K, V, BT, code, _capi.stream_of(q))
+        pq, pk, pv, pg, ph, o.data_ptr(), scale, B, T, H, K, V, BT, code, _capi.stream_of(q))
     _capi.check(status, "thm_chunk_fwd_o")
     return o
