@@ -458,6 +458,61 @@ def extension_timings(torch, inp, conv_in, iters: int = 10):
     return out
 
 
+# --------------------------------------------------------------------------- order probe
+
+def order_probe(torch, step_fns: dict, reps: int = 12) -> dict:
+    """recompute_w_u and chunk_fwd_o times after different preceding kernels
+    (HIP events per kernel, medians over ``reps`` rounds): alone back to back,
+    after a 1 GiB write (torch fill_, ordinary stores), after a 1 GiB read
+    (torch sum), after a 1 GiB copy, and inside the config-4 step.  The
+    kernels' own code and inputs are the same in every case."""
+    import statistics
+
+    dev = torch.device("cuda:0")
+    big = torch.empty(1 << 28, device=dev)
+    big2 = torch.empty_like(big)
+    pre = {"alone": None, "after 1 GiB fill": lambda: big.fill_(1.0), "after 1 GiB sum": lambda: big.sum(),
+           "after 1 GiB copy": lambda: big2.copy_(big)}
+    out = {}
+    for kname in ("recompute_w_u", "chunk_fwd_o"):
+        fn = step_fns[kname]
+        for label, p in pre.items():
+            seq = ([p] if p else []) + [fn]
+            for _ in range(3):
+                for f in seq:
+                    f()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                if p:
+                    p()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1) * 1e3)
+            out.setdefault(kname, {})[label] = round(statistics.median(ts), 1)
+    # inside the step: per-kernel events around each launch
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(reps)]
+    order = ["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o"]
+    for _ in range(2):
+        for n in order:
+            step_fns[n]()
+    torch.cuda.synchronize()
+    for r in range(reps):
+        evs[r][0].record()
+        for i, n in enumerate(order):
+            step_fns[n]()
+            evs[r][i + 1].record()
+    torch.cuda.synchronize()
+    for i, n in enumerate(order):
+        if n in out:
+            out[n]["in the step"] = round(statistics.median(evs[r][i].elapsed_time(evs[r][i + 1]) * 1e3
+                                                            for r in range(reps)), 1)
+    return out
+
+
 # --------------------------------------------------------------------------- main
 
 def main() -> int:
@@ -474,6 +529,8 @@ def main() -> int:
                     help="run only this kernel of the step (for per-kernel rocprofv3 counter runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (rocprofv3 counter calibration)")
+    ap.add_argument("--order-probe", action="store_true",
+                    help="time recompute_w_u and chunk_fwd_o after different preceding kernels, then exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the hot-path kernels are single-device; "
@@ -526,6 +583,26 @@ def main() -> int:
         o = chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=vn, g=g, h=h, scale=scale))
         mark(4)
         return y, o, ht
+
+    if args.order_probe:
+        st = {}
+
+        def _wu():
+            st["w"], st["u"] = recompute_w_u.custom_kernel(
+                recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K, V=V))
+
+        def _h():
+            st["h"], st["vn"], _ = chunk_fwd_h.custom_kernel(dict(k=k, w=st["w"], u=st["u"], g=g,
+                                                                  output_final_state=True))
+
+        fns = {"causal_conv1d": lambda: causal_conv1d.custom_kernel(conv_in), "recompute_w_u": _wu,
+               "chunk_fwd_h": _h,
+               "chunk_fwd_o": lambda: chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=st["vn"], g=g, h=st["h"],
+                                                                     scale=scale))}
+        _wu()
+        _h()
+        print(json.dumps({"order_probe_us": order_probe(torch, fns)}))
+        return 0
 
     if args.only:
         # One kernel, W + K launches on inputs from one full step (counter runs).

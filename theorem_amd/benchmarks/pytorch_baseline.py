@@ -126,18 +126,21 @@ def _stage(kname: str, shape: dict, compile_: bool):
 KERNELS = ["causal_conv1d", "chunk_fwd_h", "chunk_fwd_o", "recompute_w_u"]
 
 
-def main() -> int:
+def main(argv: List[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--kernels", default=",".join(KERNELS))
     ap.add_argument("--csv", default="gpurun_out/baseline_compare.csv")
     ap.add_argument("--no-compile", action="store_true", help="skip the torch.compile column")
-    args = ap.parse_args()
+    ap.add_argument("--max-shapes", type=int, default=0, help="only the first N benchmark shapes per kernel")
+    args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("error: no GPU device visible", file=sys.stderr)
         return 2
     rows: List[Dict[str, Any]] = []
     for kname in [s.strip() for s in args.kernels.split(",") if s.strip()]:
         shapes = yaml.safe_load((PKG / "kernels" / kname / "task.yml").read_text())["shapes"]["benchmarks"]
+        if args.max_shapes:
+            shapes = shapes[:args.max_shapes]
         print(f"\n=== {kname} ===")
         for shape in shapes:
             label = ",".join(f"{k}={v}" for k, v in shape.items() if k != "seed")
