@@ -589,7 +589,10 @@ int main() {
   H_ALL(64, 128, pipe::kHStages)
   H_ALL(128, 64, pipe::kHStages)
   H_ALL(128, 128, pipe::kHStages)
-  H_ALL(128, 128, 3)  // the general ring formulas at another depth
+  H_ALL(128, 128, 3)  // the deep rings of grids under 256 workgroups
+  H_ALL(128, 64, 3)
+  H_ALL(64, 128, 5)
+  H_ALL(64, 64, 5)
   check_h<128, 128, 1, 2, true, true, true>();  // the unsplit form
 #define F_ALL(K, V)                   \
   check_fused<K, V, true, true>();    \

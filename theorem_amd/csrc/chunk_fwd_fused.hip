@@ -305,29 +305,45 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       // waves; the accumulator of block (ib, jb) holds
       // P^T[j = 16 jb + 4 grp + r][i = 16 ib + li], so each lane stores 4
       // consecutive j of row i as one 8-byte write.
-      const uint32_t blocks = wq == 0 ? 0x0E0D0Cu : wq == 1 ? 0x0A0908u : wq == 2 ? 0xFF040Fu : 0xFF0005u;
+      // Each wave's blocks are fixed (wq is wave-uniform), so every k and q
+      // fragment a wave needs is read from LDS before its first MFMA, and
+      // only diagonal blocks are masked.  (A loop over runtime block ids
+      // read each block's fragments after the previous block's products.)
+      constexpr int KS = K / 32;
+      auto frags = [&](const char* tile, int rb, bf16x8* f) {
 #pragma unroll
-      for (int t = 0; t < 3; ++t) {
-        const int id = (int)((blocks >> (8 * t)) & 0xFF);
-        if (id == 0xFF) break;
-        const int ib = id >> 2, jb = id & 3;
+        for (int s2 = 0; s2 < KS; ++s2)
+          f[s2] = load8(reinterpret_cast<const bf16*>(tile + hl::row8_frag_off(16 * rb, 32 * s2, lane, C::kRowK)));
+      };
+      auto block = [&](int ib, int jb, const bf16x8* kf, const bf16x8* qf) {
         f32x4 pt = zero4();
 #pragma unroll
-        for (int s2 = 0; s2 < K / 32; ++s2) {
-          const bf16x8 kf = load8(reinterpret_cast<const bf16*>(tk + hl::row8_frag_off(16 * jb, 32 * s2, lane, C::kRowK)));
-          const bf16x8 qf = load8(reinterpret_cast<const bf16*>(tq + hl::row8_frag_off(16 * ib, 32 * s2, lane, C::kRowK)));
-          pt = mfma16x16x32(kf, qf, pt);
-        }
+        for (int s2 = 0; s2 < KS; ++s2) pt = mfma16x16x32(kf[s2], qf[s2], pt);
         const int i = 16 * ib + li;
+        const float gi = HAS_G ? gs[i] : 0.f;
         bf16x4 pv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = 16 * jb + 4 * grp + r;
           float gate = 1.f;
-          if constexpr (HAS_G) gate = fast_exp(gs[i] - gs[j]);
-          pv[r] = (bf16)((j <= i) ? pt[r] * gate : 0.f);
+          if constexpr (HAS_G) gate = fast_exp(gi - gs[j]);
+          pv[r] = (bf16)((jb < ib || j <= i) ? pt[r] * gate : 0.f);
         }
         *reinterpret_cast<bf16x4*>(lp + hl::pair_frag_off(16 * ib, 16 * jb, lane, 128)) = pv;
+      };
+      bf16x8 fa[KS], fb[KS], fc[KS], fd[KS];
+      if (wq == 0) {  // (3, 0), (3, 1), (3, 2)
+        frags(tq, 3, fa); frags(tk, 0, fb); frags(tk, 1, fc); frags(tk, 2, fd);
+        block(3, 0, fb, fa); block(3, 1, fc, fa); block(3, 2, fd, fa);
+      } else if (wq == 1) {  // (2, 0), (2, 1), (2, 2)
+        frags(tq, 2, fa); frags(tk, 0, fb); frags(tk, 1, fc); frags(tk, 2, fd);
+        block(2, 0, fb, fa); block(2, 1, fc, fa); block(2, 2, fd, fa);
+      } else if (wq == 2) {  // (3, 3), (1, 0)
+        frags(tq, 3, fa); frags(tk, 3, fb); frags(tq, 1, fc); frags(tk, 0, fd);
+        block(3, 3, fb, fa); block(1, 0, fd, fc);
+      } else {  // (1, 1), (0, 0)
+        frags(tq, 1, fa); frags(tk, 1, fb); frags(tq, 0, fc); frags(tk, 0, fd);
+        block(1, 1, fb, fa); block(0, 0, fd, fc);
       }
     }
     lds_barrier();  // M: P, the S pairs and the v_new pairs of chunk c are in LDS
