@@ -74,10 +74,16 @@ def _counter_kib(run_dir: str, counter: str, symbol_prefix: str) -> float:
     return sum(vals) / len(vals)
 
 
+# The runtime's device-to-device copy kernel (what `bench.py --copy-calib` runs
+# for `Tensor.copy_`); the calibration averages only its dispatches, not the
+# fill that initialises the source.
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
 def traffic_summary(calib_fetch: str, calib_write: str, copy_bytes: int, targets: dict) -> dict:
     """targets: name -> (unit, symbol_prefix, algorithmic_bytes, fetch_dir, write_dir)."""
-    cf = _counter_kib(calib_fetch, "FETCH_SIZE", "")
-    cw = _counter_kib(calib_write, "WRITE_SIZE", "")
+    cf = _counter_kib(calib_fetch, "FETCH_SIZE", COPY_KERNEL)
+    cw = _counter_kib(calib_write, "WRITE_SIZE", COPY_KERNEL)
     ff, fw = copy_bytes / 1024 / cf, copy_bytes / 1024 / cw
     out = {"_calibration": {"copy_bytes": copy_bytes, "fetch_kib_per_copy": cf, "write_kib_per_copy": cw,
                             "fetch_factor": ff, "write_factor": fw}}
