@@ -97,6 +97,28 @@ def measured_traffic(kernel: str):
                                          f"{rec['algorithmic_bytes']} B")
 
 
+def settle(torch, fn, min_s: float, batch: int = 4) -> float:
+    """Run ``fn`` (untimed) in batches until ``min_s`` seconds of wall time have
+    passed, synchronising after each batch; return the seconds spent.
+
+    The GPU comes out of an idle period (input generation, host work between
+    phases) at a lowered clock and takes tens of milliseconds of continuous work
+    to reach its steady clock: on MI355X the fused h + o kernel runs its first
+    ~30 ms after even 20 ms of idle at 400-440 us per call, against ~350 us
+    after, and the recompute_w_u -> chunk_fwd_h -> chunk_fwd_o step at
+    1150-1220 against ~1090 us.  The step and the extension kernels are timed
+    after such a settle run of the same work, so their numbers are steady-state
+    rates; the per-shape latencies keep the reference's protocol (a
+    synchronised call at a time)."""
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(batch):
+            fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= min_s:
+            return time.perf_counter() - t0
+
+
 # --------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline(torch, inputs, conv_inputs, target_s: float = 12.0):
@@ -378,11 +400,12 @@ def work_build_A(B, T, H, K, eb=2):
     return N * K * eb + N * 8 + N * 64 * 4
 
 
-def extension_timings(torch, inp, conv_in, iters: int = 10):
+def extension_timings(torch, inp, conv_in, iters: int = 10, settle_s: float = 0.05):
     """The kernels beyond the four (WY matrix, gate cumsum, channels-last conv,
     conv decode step, fused WY, fused h + o, the whole chunked forward) and the
     four in fp32 (the reference's dtype), at config-4 sizes: HIP events around
-    ``iters`` back-to-back launches after one warm-up."""
+    ``iters`` back-to-back launches after a ``settle_s`` settle run of the same
+    call."""
     from theorem_amd import chain
     from theorem_amd.kernels import causal_conv1d, recompute_w_u
 
@@ -444,8 +467,7 @@ def extension_timings(torch, inp, conv_in, iters: int = 10):
         work_o(B, T, H, K, V, eb=4)[0], f"({B},{T},{H},{K},{V}) fp32")
     out = {}
     for name, (fn, by, shape) in cases.items():
-        fn()
-        torch.cuda.synchronize()
+        settle(torch, fn, settle_s)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(iters):
@@ -513,6 +535,32 @@ def order_probe(torch, step_fns: dict, reps: int = 12) -> dict:
     return out
 
 
+# --------------------------------------------------------------------------- clock ramp probe
+
+def ramp_probe(torch, calls: dict, batches: int = 25) -> dict:
+    """Per-call time of each entry of ``calls`` (name -> (fn, calls per batch))
+    in consecutive batches after the GPU has been idle for 2 s, 0.2 s and
+    0.02 s (HIP events around each batch, a synchronize after it): how long the
+    clock takes to come out of idle, which sets the settle run before timing."""
+    out = {}
+    for name, (fn, per) in calls.items():
+        fn()
+        torch.cuda.synchronize()
+        for idle in (2.0, 0.2, 0.02):
+            time.sleep(idle)
+            ts = []
+            for _ in range(batches):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(per):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(round(e0.elapsed_time(e1) * 1e3 / per, 1))
+            out.setdefault(name, {})[f"after {idle} s idle"] = ts
+    return out
+
+
 # --------------------------------------------------------------------------- main
 
 def main() -> int:
@@ -520,6 +568,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--settle", type=float, default=0.25,
+                    help="seconds of untimed steps before the warm-up, to bring the GPU clock out of idle (0: none)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape latencies of configs 0-3")
     ap.add_argument("--no-ext", action="store_true", help="skip the extension kernels (A-builder, gate cumsum, ...)")
@@ -529,6 +579,9 @@ def main() -> int:
                     help="run only this kernel of the step (for per-kernel rocprofv3 counter runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (rocprofv3 counter calibration)")
+    ap.add_argument("--ramp-probe", action="store_true",
+                    help="per-call times of the fused h + o kernel and of the step in batches after idle periods, "
+                         "then exit")
     ap.add_argument("--order-probe", action="store_true",
                     help="time recompute_w_u and chunk_fwd_o after different preceding kernels, then exit")
     args = ap.parse_args()
@@ -604,6 +657,14 @@ def main() -> int:
         print(json.dumps({"order_probe_us": order_probe(torch, fns)}))
         return 0
 
+    if args.ramp_probe:
+        w0, u0 = recompute_w_u.custom_kernel(recompute_w_u.Data(k=k, v=v, beta=beta, A=A, g=g, B=B, T=T, H=H, K=K,
+                                                                V=V))
+        calls = {"chunk_gated_delta_fwd": (lambda: chain.chunk_fwd_fused(q, k, w0, u0, g, scale, None, True), 10),
+                 "step": (step, 5)}
+        print(json.dumps({"ramp_probe_us_per_call": ramp_probe(torch, calls)}))
+        return 0
+
     if args.only:
         # One kernel, W + K launches on inputs from one full step (counter runs).
         y, o, ht = step()
@@ -626,6 +687,7 @@ def main() -> int:
         print(json.dumps({"only": args.only, "launches": args.warmup + args.steps + 1}))
         return 0
 
+    settled_s = settle(torch, step, args.settle) if args.settle > 0 else 0.0
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -700,7 +762,8 @@ def main() -> int:
                 f"chunk fwd recompute_w_u->chunk_fwd_h->chunk_fwd_o B={B},T={T},H={H},K={K},V={V},BT=64 bf16")
     line = {
         "metric": METRIC, "value": round(ms_per_step * 1e3, 2), "unit": "µs/call", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "steps": args.steps, "warmup": args.warmup, "settle_s": round(settled_s, 3),
+        "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded torch CPU generator; BASELINE.json config-4 distributions)",
         "config": {"workload": workload, "parallelism": "single GPU"},
