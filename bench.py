@@ -103,10 +103,10 @@ def settle(torch, fn, min_s: float, batch: int = 4) -> float:
 
     The GPU comes out of an idle period (input generation, host work between
     phases) at a lowered clock and takes tens of milliseconds of continuous work
-    to reach its steady clock: on MI355X the fused h + o kernel runs its first
-    ~30 ms after even 20 ms of idle at 400-440 us per call, against ~350 us
-    after, and the recompute_w_u -> chunk_fwd_h -> chunk_fwd_o step at
-    1150-1220 against ~1090 us.  The step and the extension kernels are timed
+    to reach its steady clock (``--ramp-probe``): on MI355X the fused h + o
+    kernel runs its first ~10 ms after even 20 ms of idle at 395-425 us per
+    call, against ~345 us after ~35 ms, and the config-4 step at 1367-1387
+    against ~1287 us.  The step and the extension kernels are timed
     after such a settle run of the same work, so their numbers are steady-state
     rates; the per-shape latencies keep the reference's protocol (a
     synchronised call at a time)."""
