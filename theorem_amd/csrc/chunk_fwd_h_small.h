@@ -134,12 +134,16 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) put_out(ho, kb, S[kb]);  // h[c]: state before chunk c
       }
-      // v_new (or v) for rows j = 16 jb + 4 grp + r of this lane's column.
+      // v_new (or v) for rows j = 16 jb + 4 grp + r of this lane's column: one
+      // transposed read per 16-row block (lane li of a 16-lane group receives
+      // the 4 rows of column 16 wq + li).
       f32x4 vn[4];
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb)
+      for (int jb = 0; jb < 4; ++jb) {
+        const bf16x4 u4 = ds_read_tr16(us + (16 * jb + 4 * grp + (li >> 2)) * C::kUPitch + 16 * wv + 4 * (li & 3));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vn[jb][r] = to_f32(us[(16 * jb + 4 * grp + r) * C::kUPitch + ucol]);
+        for (int r = 0; r < 4; ++r) vn[jb][r] = to_f32(u4[r]);
+      }
       if constexpr (DELTA) {
         // P1: B operand = S pairs (kappa blocks 2t, 2t+1) in paired order.
         const bf16* const ws = st_w(s);
