@@ -339,7 +339,12 @@ static void check_fused() {
       const int base = s * C::kStage;
       for (int m = 0; m < 3; ++m) reg.push_back({base + m * C::kTileK, base + (m + 1) * C::kTileK});
       reg.push_back({base + 3 * C::kTileK, base + 3 * C::kTileK + C::kTileU});
-      if (HAS_G) reg.push_back({base + 3 * C::kTileK + C::kTileU, base + 3 * C::kTileK + C::kTileU + 256});
+      if (HAS_G) {
+        // gates (DMA), then e^{g_i} and e^{g_last - g_j} (written by state wave 0)
+        const int gb = base + 3 * C::kTileK + C::kTileU;
+        for (int part = 0; part < 3; ++part) reg.push_back({gb + 256 * part, gb + 256 * (part + 1)});
+        CHECK(3 * 256 <= C::kGBytes, "%s: gate block", what);
+      }
     }
     const int lp = pipe::kFStages * C::kStage;
     reg.push_back({lp, lp + C::kPBytes});

@@ -258,6 +258,19 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 
     f32x4 vn[4];    // state waves: v_new rows j = 16 jb + 4 grp + r of column 16 wq + li
     bf16x8 vp[2];   // state waves: v_new as bf16 B-operand pairs
+    if constexpr (HAS_G) {
+      // The chunk's gate factors, once per workgroup (state wave 0, one token
+      // per lane), into the stage's gate block after the gates (which the DMA
+      // fills, bytes 0-255): e^{g_i} for the output's global term at +64
+      // floats, e^{g_last - g_j} for the state update at +128.  Read after
+      // barrier M; the next write is after the next barrier A.
+      if (state_wave && wq == 0) {
+        float* const ge = stage_g(s);
+        const float gt = ge[lane];
+        ge[64 + lane] = fast_exp(gt);
+        ge[128 + lane] = fast_exp(ge[kBT - 1] - gt);
+      }
+    }
     if (state_wave) {
       // The next chunk's DMA is issued in four parts between P1's row blocks,
       // so the address unit drains between parts while the MFMAs run.
@@ -353,16 +366,16 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       bf16x8 vh[2];
       float decay = 1.f;
       if constexpr (HAS_G) {
-        const float gl = gs[kBT - 1];
-        decay = fast_exp(gl);
+        decay = fast_exp(gs[kBT - 1]);
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
+          const f32x4 fa = *reinterpret_cast<const f32x4*>(gs + 128 + 32 * s2 + 4 * grp);  // e^{g_last - g_j}
+          const f32x4 fb = *reinterpret_cast<const f32x4*>(gs + 128 + 32 * s2 + 16 + 4 * grp);
           float f[8];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int j0 = 32 * s2 + 4 * grp + r;
-            f[r] = vn[2 * s2][r] * fast_exp(gl - gs[j0]);
-            f[4 + r] = vn[2 * s2 + 1][r] * fast_exp(gl - gs[j0 + 16]);
+            f[r] = vn[2 * s2][r] * fa[r];
+            f[4 + r] = vn[2 * s2 + 1][r] * fb[r];
           }
           vh[s2] = to_bf16x8(f);
         }
@@ -391,8 +404,9 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       for (int ib = 0; ib < 4; ++ib) {
         f32x4 acc = rows_times_S(tq, ib, sb);  // q S
         if constexpr (HAS_G) {
+          const f32x4 e = *reinterpret_cast<const f32x4*>(gs + 64 + 16 * ib + 4 * grp);  // e^{g_i}
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] *= fast_exp(gs[16 * ib + 4 * grp + r]);
+          for (int r = 0; r < 4; ++r) acc[r] *= e[r];
         }
         // Local term: A = P[i][j] rows of lp, B = v_new (pairs), paired order
         // over j; key blocks above the diagonal block contribute zero.
