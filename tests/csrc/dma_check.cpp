@@ -390,8 +390,8 @@ static void check_fused() {
                      tsv, 2, what);
     co.exactly_once(what);
   }
-  // Wait counts of the memory waves: prologue DMA(0) + prefetch; per chunk the
-  // DMA of c + 1, the prefetch of c + 2 (their only vector memory ops).
+  // Wait counts of the state waves: prologue DMA(0) + prefetch; per chunk the
+  // DMA of c + 1 (4 parts), the prefetch of c + 2, the v_new stores of c.
   for (int NT = 1; NT <= 5; ++NT)
     for (int wq = 0; wq < 4; ++wq) {
       WaveOps w;
@@ -399,9 +399,10 @@ static void check_fused() {
       w.dma(0, nd);
       w.other(C::kPf);
       for (int c = 0; c < NT; ++c) {
-        w.check_wait(c, C::kWaitDma, what, c);
+        w.check_wait(c, c < pipe::kFStages - 1 ? C::kWaitFirst : C::kWaitSteady, what, c);
         w.dma(c + 1 < NT ? c + 1 : -2, nd);
         w.other(C::kPf);
+        w.other(C::kStores);
       }
     }
 }

@@ -92,9 +92,9 @@ MUTATIONS = [
     ("pipe_cfg.h", "static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma;",
      "static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma + 1;",
      "chunk_fwd_h: steady-state wait one op too loose"),
-    ("pipe_cfg.h", "static constexpr int kWaitDma = kPf;",
-     "static constexpr int kWaitDma = kPf + 1;",
-     "fused: memory-wave wait one op too loose"),
+    ("pipe_cfg.h", "static constexpr int kWaitSteady = kPf + kStores;",
+     "static constexpr int kWaitSteady = kPf + kStores - 1;",
+     "fused: steady-state wait one op too tight"),
 ]
 
 

@@ -12,13 +12,12 @@
 // state before chunk c; nothing of either reference kernel's output but o
 // (and optionally v_new and the final state) is written.
 //
-// Structure: one 768-thread workgroup per (b, head, V-tile), 12 wavefronts in
-// three roles, one of each per SIMD; wave role and column group wq (columns
+// Structure: one 512-thread workgroup per (b, head, V-tile), 8 wavefronts in
+// two roles that share SIMDs pairwise; wave role and column group wq (columns
 // 16 wq .. 16 wq + 15 of the tile) are wave-uniform:
 //   * k, w, q, u and g of a chunk arrive by global -> LDS DMA into a 2-stage
 //     ring (XOR-swizzled tiles of h_layout.h), one chunk ahead of use, issued
-//     by the memory waves (8-11), which also prefetch the chunk after it into
-//     L2 and compute the chunk's gate factors once per workgroup;
+//     by the state waves;
 //   * state waves (0-3) hold S[K x 16 columns] in fp32 registers.  Phase 1:
 //     hand S to the output waves as bf16 B-operand pairs (LDS), P1 v_new =
 //     u - w S (the S pairs as the B operand, paired contraction order), hand
@@ -33,10 +32,9 @@
 //     4x4 quad transpose;
 //   * a barrier at the top of each chunk (its tiles are in LDS, chunk c - 1
 //     is finished) and one between the phases.
-// All DMA and stores of the chunk loop go through vmem.h.  Only the memory
-// waves issue DMA, and nothing else, so their wait at the top of the loop is
-// an exact count (the L2 prefetch issued after each chunk's DMA); the state
-// and output waves issue stores only.
+// All DMA and stores of the chunk loop go through vmem.h, and the state waves'
+// wait at the top of the loop is an exact count (their v_new stores of one
+// chunk are issued after each chunk's DMA); the output waves issue stores only.
 // HBM traffic per token-head: k, w and q (K eb each), u (V eb) and g (4 B)
 // read once; o (V eb) written once (+ v_new when requested).  The V-tiles of
 // one (b, head) run on one XCD, so their second read of k, w, q is meant to
@@ -75,10 +73,8 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 
   const int tid = threadIdx.x;
   const int wi = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool state_wave = wi < 4;              // waves 0-3: recurrence
-  const bool out_wave = wi >= 4 && wi < 8;      // waves 4-7: output
-  const bool mem_wave = wi >= 8;                // waves 8-11: the DMA ring
-  const int wq = wi & 3;  // column group 16 wq .. 16 wq + 15 of the tile; a memory wave's DMA share
+  const bool state_wave = wi < 4;  // waves 0-3: recurrence; waves 4-7: output
+  const int wq = wi & 3;           // column group 16 wq .. 16 wq + 15 of the tile
   const int lane = tid & 63, grp = lane >> 4, li = lane & 15;
 
   auto stage_k = [&](int s) { return lds + s * C::kStage; };
@@ -114,7 +110,30 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   }
   const uint32_t goff = (uint32_t)(lane * H * 4);
 
-  // DMA of chunk cc into stage s; issued by the memory waves only.
+  // Part m of the DMA of chunk cc into stage s: m = 0, 1, 2 the k, w, q tile,
+  // m = 3 the u tile and the gates.
+  auto issue_part = [&](int64_t cc, int s, int m) {
+    const int64_t off = kc0 + cc * kcs;
+    if (m < 3) {
+      const char* src = reinterpret_cast<const char*>(m == 0 ? k : m == 1 ? w : q) + off;
+      char* dst = m == 0 ? stage_k(s) : m == 1 ? stage_w(s) : stage_q(s);
+      const uint32_t l0 = lds_address(dst) + wq * C::kKDma * 1024;
+#pragma unroll
+      for (int i = 0; i < C::kKDma; ++i) dma_b128(src, koff[i], __builtin_amdgcn_readfirstlane(l0 + i * 1024));
+    } else {
+      const char* ub = reinterpret_cast<const char*>(u) + uc0 + cc * ucs;
+      const uint32_t lu = lds_address(stage_u(s)) + wq * C::kUDma * 1024;
+#pragma unroll
+      for (int i = 0; i < C::kUDma; ++i) dma_b128(ub, uoff[i], __builtin_amdgcn_readfirstlane(lu + i * 1024));
+      if constexpr (HAS_G) {
+        if (wq == 0) {
+          const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
+          dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s))));
+        }
+      }
+    }
+  };
+  // DMA of chunk cc into stage s; issued by the state waves only.
   auto issue = [&](int64_t cc, int s) {
     const int64_t off = kc0 + cc * kcs;
     const char* srcs[3] = {reinterpret_cast<const char*>(k) + off, reinterpret_cast<const char*>(w) + off,
@@ -140,7 +159,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     }
   };
 
-  // L2 prefetch of chunk cc (memory waves): one 4-byte DMA per 64-byte line of
+  // L2 prefetch of chunk cc (state waves): one 4-byte DMA per 64-byte line of
   // the chunk's tiles, landing in a scratch LDS slot whose contents are never
   // read, so the DMA of that chunk one iteration later finds its lines in L2.
   // Waves 0, 1, 2 cover the k, w, q rows (up to 256 lines each), wave 3 the
@@ -222,47 +241,42 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       S[kb][r] = (state_wave && h0) ? h0[st_base + (int64_t)(16 * kb + 4 * grp + r) * V + ncol] : 0.f;
   wait_vmcnt<0>();  // retire the h0 loads before the counted loop
 
-  // One loop per role, each passing the same two barriers per chunk (A: the
-  // chunk's tiles are in LDS and every wave is done with chunk c - 1; M: the
-  // scores, the S pairs and the v_new pairs of chunk c are in LDS), so that
-  // no role's registers are live in another role's loop.
-  if (mem_wave) {
-    if (NT > 0) {
-      issue(0, 0);
-      prefetch(NT > 1 ? 1 : 0);
+  if (state_wave && NT > 0) {
+    issue(0, 0);
+    prefetch(NT > 1 ? 1 : 0);
+  }
+  for (int64_t c = 0; c < NT; ++c) {
+    const int s = (int)(c % kFStages);
+    if (state_wave) {
+      if (c < kFStages - 1) wait_vmcnt<C::kWaitFirst>();
+      else wait_vmcnt<C::kWaitSteady>();
     }
-    for (int64_t c = 0; c < NT; ++c) {
-      const int s = (int)(c % kFStages);
-      wait_vmcnt<C::kWaitDma>();  // this wave's DMA of chunk c has landed
-      lds_barrier();  // A
-      if constexpr (HAS_G) {
-        // The chunk's gate factors, once per workgroup (memory wave 8, one
-        // token per lane), into the stage's gate block after the gates
-        // (which the DMA fills, bytes 0-255): e^{g_i} for the output's global
-        // term at +64 floats, e^{g_last - g_j} for the state update at +128.
-        // Read after barrier M; the next write is after the next barrier A.
-        if (wq == 0) {
-          float* const ge = stage_g(s);
-          const float gt = ge[lane];
-          ge[64 + lane] = fast_exp(gt);
-          ge[128 + lane] = fast_exp(ge[kBT - 1] - gt);
-        }
+    lds_barrier();  // A: chunk c is in LDS; every wave is done with chunk c - 1
+    const char* tk = stage_k(s);
+    const char* tq = stage_q(s);
+    const float* gs = HAS_G ? stage_g(s) : nullptr;
+
+    f32x4 vn[4];    // state waves: v_new rows j = 16 jb + 4 grp + r of column 16 wq + li
+    bf16x8 vp[2];   // state waves: v_new as bf16 B-operand pairs
+    if constexpr (HAS_G) {
+      // The chunk's gate factors, once per workgroup (state wave 0, one token
+      // per lane), into the stage's gate block after the gates (which the DMA
+      // fills, bytes 0-255): e^{g_i} for the output's global term at +64
+      // floats, e^{g_last - g_j} for the state update at +128.  Read after
+      // barrier M; the next write is after the next barrier A.
+      if (state_wave && wq == 0) {
+        float* const ge = stage_g(s);
+        const float gt = ge[lane];
+        ge[64 + lane] = fast_exp(gt);
+        ge[128 + lane] = fast_exp(ge[kBT - 1] - gt);
       }
-      // The next chunk's DMA (the stage chunk c - 1 used), then the L2
-      // prefetch of the chunk after it.
-      const int64_t cn = c + kFStages - 1;
-      issue(cn < NT ? cn : NT - 1, (int)(cn % kFStages));
-      prefetch(cn + 1 < NT ? cn + 1 : NT - 1);
-      lds_barrier();  // M
     }
-  } else if (state_wave) {
-    for (int64_t c = 0; c < NT; ++c) {
-      const int s = (int)(c % kFStages);
-      lds_barrier();  // A
-      const char* tk = stage_k(s);
-      const float* gs = HAS_G ? stage_g(s) : nullptr;
-      f32x4 vn[4];    // v_new rows j = 16 jb + 4 grp + r of column 16 wq + li
-      bf16x8 vp[2];   // v_new as bf16 B-operand pairs
+    if (state_wave) {
+      // The next chunk's DMA is issued in four parts between P1's row blocks,
+      // so the address unit drains between parts while the MFMAs run.
+      const int64_t cn = c + kFStages - 1;
+      const int64_t cnc = cn < NT ? cn : NT - 1;
+      const int cns = (int)(cn % kFStages);
       // S as the B operand (pairs of 16-row tiles), also handed to the output wave.
       bf16x8 sb[KB2];
 #pragma unroll
@@ -277,11 +291,13 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       const char* tu = stage_u(s);
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
+        issue_part(cnc, cns, jb);
         const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(tu + hl::tr_frag_off(16 * jb, 16 * wq, lane, C::kRowU)));
 #pragma unroll
         for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
         vn[jb] -= rows_times_S(tw, jb, sb);
       }
+      prefetch(cn + 1 < NT ? cn + 1 : NT - 1);
       if constexpr (STORE_VN) {
         bf16* vb = vnew + ((b * T + c * kBT) * H + hh) * V;
 #pragma unroll
@@ -295,46 +311,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
         vp[s2] = to_bf16x8(f);
         lv[s2 * 64] = vp[s2];
       }
-      lds_barrier();  // M
-      // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
-      bf16x8 vh[2];
-      float decay = 1.f;
-      if constexpr (HAS_G) {
-        decay = fast_exp(gs[kBT - 1]);
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const f32x4 fa = *reinterpret_cast<const f32x4*>(gs + 128 + 32 * s2 + 4 * grp);  // e^{g_last - g_j}
-          const f32x4 fb = *reinterpret_cast<const f32x4*>(gs + 128 + 32 * s2 + 16 + 4 * grp);
-          float f[8];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            f[r] = vn[2 * s2][r] * fa[r];
-            f[4 + r] = vn[2 * s2 + 1][r] * fb[r];
-          }
-          vh[s2] = to_bf16x8(f);
-        }
-      } else {
-        vh[0] = vp[0];
-        vh[1] = vp[1];
-      }
-#pragma unroll
-      for (int kb = 0; kb < C::KB; ++kb) {
-        if constexpr (HAS_G) S[kb] *= decay;
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const bf16x4 a = ds_read_tr16(reinterpret_cast<const bf16*>(tk + hl::tr_frag_off(32 * s2, 16 * kb, lane, C::kRowK)));
-          const bf16x4 bq = ds_read_tr16(reinterpret_cast<const bf16*>(tk + hl::tr_frag_off(32 * s2 + 16, 16 * kb, lane, C::kRowK)));
-          S[kb] = mfma16x16x32(concat(a, bq), vh[s2], S[kb]);
-        }
-      }
-    }
-  } else {  // output waves
-    for (int64_t c = 0; c < NT; ++c) {
-      const int s = (int)(c % kFStages);
-      lds_barrier();  // A
-      const char* tk = stage_k(s);
-      const char* tq = stage_q(s);
-      const float* gs = HAS_G ? stage_g(s) : nullptr;
+    } else {
       // Scores, once per workgroup: P[i][j] = (q_i . k_j) e^{g_i - g_j} for
       // j <= i (0 above the diagonal), as bf16 rows of lp.  The ten 16 x 16
       // blocks (ib, jb <= ib) are shared out 3 / 3 / 2 / 2 over the output
@@ -381,7 +358,42 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
         frags(tq, 1, fa); frags(tk, 1, fb); frags(tq, 0, fc); frags(tk, 0, fd);
         block(1, 1, fb, fa); block(0, 0, fd, fc);
       }
-      lds_barrier();  // M
+    }
+    lds_barrier();  // M: P, the S pairs and the v_new pairs of chunk c are in LDS
+
+    if (state_wave) {
+      // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
+      bf16x8 vh[2];
+      float decay = 1.f;
+      if constexpr (HAS_G) {
+        decay = fast_exp(gs[kBT - 1]);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const f32x4 fa = *reinterpret_cast<const f32x4*>(gs + 128 + 32 * s2 + 4 * grp);  // e^{g_last - g_j}
+          const f32x4 fb = *reinterpret_cast<const f32x4*>(gs + 128 + 32 * s2 + 16 + 4 * grp);
+          float f[8];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            f[r] = vn[2 * s2][r] * fa[r];
+            f[4 + r] = vn[2 * s2 + 1][r] * fb[r];
+          }
+          vh[s2] = to_bf16x8(f);
+        }
+      } else {
+        vh[0] = vp[0];
+        vh[1] = vp[1];
+      }
+#pragma unroll
+      for (int kb = 0; kb < C::KB; ++kb) {
+        if constexpr (HAS_G) S[kb] *= decay;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const bf16x4 a = ds_read_tr16(reinterpret_cast<const bf16*>(tk + hl::tr_frag_off(32 * s2, 16 * kb, lane, C::kRowK)));
+          const bf16x4 bq = ds_read_tr16(reinterpret_cast<const bf16*>(tk + hl::tr_frag_off(32 * s2 + 16, 16 * kb, lane, C::kRowK)));
+          S[kb] = mfma16x16x32(concat(a, bq), vh[s2], S[kb]);
+        }
+      }
+    } else {
       // Output, one 16-row query block at a time: o = scale (e^{g_i} q S + P v_new).
       bf16x8 sb[KB2];
 #pragma unroll

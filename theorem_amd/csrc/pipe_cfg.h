@@ -56,12 +56,11 @@ struct PCfg {
 };
 
 // ---------------------------------------------------------------------------
-// Fused h + o kernel: 12 wavefronts, state waves 0-3, output waves 4-7 and
-// memory waves 8-11; wave wq = w % 4 on columns 16 wq .. + 15 of the V-tile
-// (state, output) or with share wq of the DMA (memory).  Per chunk c the
-// memory waves issue the DMA of chunk c + 1 (k, w, q, u and the gates) and an
-// L2 prefetch of chunk c + 2, nothing else.
-constexpr int kFThreads = 768;     // 4 state + 4 output + 4 memory wavefronts
+// Fused h + o kernel: 8 wavefronts, state waves 0-3 and output waves 4-7, wave
+// wq = w % 4 on columns 16 wq .. + 15 of the V-tile.  The state waves issue the
+// DMA of chunk c + 1 (k, w, q, u and the gates, in four parts), an L2
+// prefetch of chunk c + 2 and their v_new stores of chunk c.
+constexpr int kFThreads = 512;     // 4 state + 4 output wavefronts
 constexpr int kFStages = 2;
 constexpr bool kFPrefetch = true;  // L2 prefetch of the chunk after the one in flight
 
@@ -79,17 +78,19 @@ struct FCfg {
   static constexpr int kVBytes = 4 * 2 * 64 * 16;         // v_new handed over the same way
   static constexpr int kTrash = 256;                      // landing slot of the L2 prefetch DMAs
   static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes + kTrash;
-  static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per memory wave per k / w / q tile
+  static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per state wave per k / w / q tile
   static constexpr int kUDma = kTileU / 1024 / 4;
   static constexpr int kDma = 3 * kKDma + kUDma + (HAS_G ? 1 : 0);
-  static constexpr int kPf = kFPrefetch ? 4 : 0;    // L2 prefetch DMAs per memory wave per chunk
-  // Ops a memory wave issues after the DMA of chunk c before it waits for it:
-  // the prefetch of chunk c + 1.
-  static constexpr int kWaitDma = kPf;
+  static constexpr int kStores = STORE_VN ? 4 : 0;  // v_new row tiles per state wave
+  static constexpr int kPf = kFPrefetch ? 4 : 0;    // L2 prefetch DMAs per state wave per chunk
+  // Ops a state wave issues after the DMA of chunk c before it waits for it:
+  // the prefetch of chunk c + 1 (and, from c = 1 on, the stores of chunk c - 1).
+  static constexpr int kWaitFirst = kPf;
+  static constexpr int kWaitSteady = kPf + kStores;
   static_assert(kFStages == 2, "the wait counts assume double buffering");
   static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
   static_assert(kLds <= 160 * 1024, "LDS budget");
-  static_assert(kWaitDma <= 63, "vmcnt range");
+  static_assert(kWaitSteady <= 63, "vmcnt range");
 };
 
 }  // namespace pipe
