@@ -52,6 +52,12 @@ UNIT_FLAGS = {
 FLOORS_SRC = "floors.hip"
 FLOORS_LIB = LIB_DIR / "libtheorem_floors.so"
 
+# Host fast path of the custom_kernel wrappers: a pybind11 module over torch
+# tensors, linked against the C-ABI library (theorem_amd/kernels/_capi.py
+# loads it when present; the wrappers' ctypes path is the same kernels).
+FAST_SRC = "host/fastpath.cpp"
+FAST_NAME = "_fastpath"
+
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed-fp32 VALU ops are disabled for all device code; the host pass warns
@@ -87,7 +93,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     OBJ_DIR.mkdir(exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
-    missing = [s for s in SOURCES + [FLOORS_SRC] if not (CSRC / s).exists()]
+    missing = [s for s in SOURCES + [FLOORS_SRC, FAST_SRC] if not (CSRC / s).exists()]
     if missing:
         raise RuntimeError(f"missing sources in {CSRC}: {', '.join(missing)}")
     srcs = [CSRC / s for s in SOURCES]
@@ -101,12 +107,43 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         for f in futs:
             f.result()
     tmp = LIB_DIR / (LIB_NAME + ".tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{LIB_NAME}", "-o", str(tmp),
+          *map(str, objs)], verbose)
     os.replace(tmp, LIB_PATH)
     ftmp = LIB_DIR / (FLOORS_LIB.name + ".tmp")
     _run([HIPCC, *COMMON_FLAGS, "-shared", "-o", str(ftmp), str(CSRC / FLOORS_SRC)], verbose)
     os.replace(ftmp, FLOORS_LIB)
+    build_fastpath(verbose)
     return LIB_PATH
+
+
+def fastpath_path() -> Path:
+    import sysconfig
+
+    return LIB_DIR / (FAST_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_fastpath(verbose: bool = False) -> Path:
+    """g++ the pybind11 fast-path module against torch's headers and libraries
+    and the C-ABI library (rpath $ORIGIN: both live in theorem_amd/lib)."""
+    import sysconfig
+
+    import torch.utils.cpp_extension as ce
+
+    out = fastpath_path()
+    tmp = out.with_name(out.name + ".tmp")
+    torch_lib = ce.library_paths()[0]
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__",
+           "-DTORCH_EXTENSION_NAME=" + FAST_NAME, "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-I/opt/rocm/include", f"-I{PKG.parent / 'include'}",
+           *(f"-I{p}" for p in ce.include_paths()), f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / FAST_SRC), "-o", str(tmp),
+           f"-L{LIB_DIR}", "-ltheorem_mi355x", f"-L{torch_lib}",
+           "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+    _run(cmd, verbose)
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

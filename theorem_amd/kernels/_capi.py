@@ -84,6 +84,37 @@ def load_library(path: Path | str | None = None) -> ctypes.CDLL:
         return lib
 
 
+_fast = None
+
+
+def fastpath():
+    """The host fast-path module of the wrappers (``theorem_amd/lib/_fastpath*.so``,
+    built by theorem_amd.build: argument checks, output allocation and the C-ABI
+    launch of a call in C++), or None when it is not built or does not load.
+    Its functions return None for any call outside the common case; the
+    wrappers then take their ctypes path to the same kernels."""
+    global _fast
+    if _fast is None:
+        _fast = False
+        try:
+            import importlib.machinery
+            import importlib.util
+
+            from ..build import fastpath_path
+
+            p = fastpath_path()
+            if p.exists():
+                load_library()  # the C-ABI library first: the module links against it by soname
+                loader = importlib.machinery.ExtensionFileLoader("_fastpath", str(p))
+                spec = importlib.util.spec_from_file_location("_fastpath", str(p), loader=loader)
+                mod = importlib.util.module_from_spec(spec)
+                loader.exec_module(mod)
+                _fast = mod
+        except (ImportError, OSError):
+            _fast = False
+    return _fast or None
+
+
 def status_string(status: int) -> str:
     return load_library().thm_status_string(int(status)).decode()
 

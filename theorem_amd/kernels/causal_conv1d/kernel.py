@@ -57,6 +57,12 @@ def custom_kernel(data: tuple, activation: str | None = None) -> torch.Tensor:
         out [B, D, S], dtype and layout of x (``torch.empty_like(x)``).
     """
     x, weight, bias = data
+    act = _ACT.get(activation)
+    fp = _capi.fastpath() if act is not None else None
+    if fp is not None:
+        out = fp.conv1d(x, weight, bias, act)
+        if out is not None:
+            return out
     B, D, S = x.shape
     channels_last = not x.is_contiguous() and _is_channels_last(x)
     assert x.is_contiguous() or channels_last, "x must be contiguous (B, D, S) or channels-last"

@@ -39,6 +39,13 @@ def custom_kernel(data):
     for key, val in (("B", B), ("T", T), ("H", H), ("K", K), ("V", V)):
         if key in data and data[key] != val:
             raise AssertionError(f"data[{key!r}]={data[key]} disagrees with the tensors ({val})")
+    fp = _capi.fastpath()
+    if fp is not None:
+        r = fp.h(k, w, vu, g, h0, delta, want_vn, want_ht)
+        if r is not None:
+            if delta:
+                return r
+            return (r[0], r[2]) if want_ht else r[0]
     assert T % CHUNK_SIZE == 0, f"T={T} must be divisible by {CHUNK_SIZE}"
     NT = T // CHUNK_SIZE
     if vu.shape[:3] != (B, T, H) or (w is not None and w.shape != k.shape) or (

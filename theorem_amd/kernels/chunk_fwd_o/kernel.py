@@ -22,6 +22,11 @@ def custom_kernel(data: Dict[str, Any]) -> torch.Tensor:
     """o = scale (mask_incl(q k^T e^{g_i - g_j}) v + e^{g} q h[c]); o [B, T, H, V]."""
     q, k, v, g, h = data["q"], data["k"], data["v"], data.get("g"), data["h"]
     scale = float(data["scale"])
+    fp = _capi.fastpath()
+    if fp is not None:
+        o = fp.o(q, k, v, g, h, scale)
+        if o is not None:
+            return o
     B, T, H, K = q.shape
     V = v.shape[-1]
     NT = h.shape[1]

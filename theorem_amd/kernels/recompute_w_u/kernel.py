@@ -38,6 +38,11 @@ SHAPE_CONFIGS = {
 
 
 def _launch(k, v, beta, A, g):
+    fp = _capi.fastpath()
+    if fp is not None:
+        r = fp.wu(k, v, beta, A, g)
+        if r is not None:
+            return r
     B, T, H, K = k.shape
     V = v.shape[-1]
     bth = (B, T, H)
