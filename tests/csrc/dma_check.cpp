@@ -1,5 +1,6 @@
 // Host-side check of the addressing of the two global -> LDS DMA pipelines
-// (the bf16 chunk_fwd_h kernel and the fused h + o kernel), built with g++ and
+// (the bf16 chunk_fwd_h kernel and the fused h + o kernel) and of the
+// small-grid chunk_fwd_h kernel's register-staged tiles and out buffers, built with g++ and
 // run by tests/test_dma_layout.py.  It evaluates the index functions the
 // kernels call (theorem_amd/csrc/h_layout.h) and the layout constants they
 // use (theorem_amd/csrc/pipe_cfg.h) for every instantiation, and checks:
@@ -407,6 +408,110 @@ static void check_fused() {
     }
 }
 
+// --------------------------------------------------------------------------- small-grid chunk_fwd_h
+
+// The register-staged small-grid kernel (chunk_fwd_h_small.h): the memory
+// waves' loads cover each tile's 8-element pieces exactly once, from inside the
+// chunk's token block and the V-tile, into aligned slots of the padded LDS
+// tiles; the state waves' out-buffer writes cover the h and v_new tiles exactly
+// once, conflict-free per instruction; the memory waves' 16-byte out-buffer
+// reads and their stores cover the same tiles exactly once.
+template <int K, int V, int NW, bool DELTA>
+static void check_small() {
+  using C = pipe::SCfg<K, NW, DELTA>;
+  char what[128];
+  std::snprintf(what, sizeof what, "small chunk_fwd_h K=%d V=%d NW=%d delta=%d", K, V, NW, DELTA);
+  {
+    std::vector<std::pair<int, int>> reg;
+    for (int s = 0; s < 2; ++s) {
+      const int base = s * C::kStageB;
+      reg.push_back({base, base + C::kKTileB});
+      if (DELTA) reg.push_back({base + C::kKTileB, base + 2 * C::kKTileB});
+      const int ub = base + C::kKTileB * (DELTA ? 2 : 1);
+      reg.push_back({ub, ub + C::kUTileB});
+      reg.push_back({ub + C::kUTileB, ub + C::kUTileB + 65 * 4});  // 64 factors + e^{g_last}
+      CHECK(ub + C::kUTileB + C::kGateB == base + C::kStageB, "%s: stage %d size", what, s);
+    }
+    const int ob = 2 * C::kStageB;
+    for (int s = 0; s < 2; ++s) reg.push_back({ob + s * C::kHOutB, ob + (s + 1) * C::kHOutB});
+    for (int s = 0; s < 2 && DELTA; ++s)
+      reg.push_back({ob + 2 * C::kHOutB + s * C::kVOutB, ob + 2 * C::kHOutB + (s + 1) * C::kVOutB});
+    for (size_t i = 0; i < reg.size(); ++i) {
+      CHECK(reg[i].first % 16 == 0 && reg[i].second <= C::kLds, "%s: LDS region %zu", what, i);
+      for (size_t j = 0; j < i; ++j)
+        CHECK(reg[i].first >= reg[j].second || reg[j].first >= reg[i].second, "%s: LDS regions %zu and %zu overlap",
+              what, i, j);
+    }
+  }
+  // Loads: (tile width n, pieces per lane, LDS pitch in elements, LDS tile bytes).
+  const int tiles[2][4] = {{K, C::kKLoads, C::kKPitch, C::kKTileB}, {C::kCols, C::kULoads, C::kUPitch, C::kUTileB}};
+  for (const auto& t : tiles) {
+    const int n = t[0], per = t[1], pitch = t[2], tb = t[3];
+    Cover cv(64, n / 8);
+    for (int m = 0; m < C::kML; ++m)
+      for (int it = 0; it < per; ++it) {
+        const int row = hl::spiece_row(m, it, n, C::kML), col = hl::spiece_col(m, n);
+        CHECK(col % 8 == 0 && col + 8 <= n, "%s: piece column %d outside [0, %d)", what, col, n);
+        cv.add(row, col / 8, what);
+        const int a = (row * pitch + col) * 2;
+        CHECK(a % 16 == 0 && a + 16 <= tb, "%s: LDS slot %d of a %d-byte tile", what, a, tb);
+      }
+    cv.exactly_once(what);
+  }
+  // Global bounds of the loads and stores at the extreme (b, head, chunk, V-tile).
+  for (const Shape& sh : kShapes) {
+    const int64_t NT = sh.T / 64, b = sh.B - 1, hh = sh.H - 1, c = NT - 1, v0 = V - C::kCols;
+    const int64_t tok_k = sh.H * K, tok_v = sh.H * V;
+    const int64_t kmax = ((b * sh.T + c * 64 + hl::spiece_row(C::kML - 1, C::kKLoads - 1, K, C::kML)) * sh.H + hh) * K +
+                         hl::spiece_col(C::kML - 1, K) + 8;
+    CHECK(kmax <= sh.B * sh.T * sh.H * K, "%s: k / w load past the tensor", what);
+    int64_t umax = 0, hmax = 0, vmax = 0;
+    for (int m = 0; m < C::kML; ++m)
+      for (int it = 0; it < C::kULoads; ++it)
+        umax = std::max(umax, ((b * sh.T + c * 64 + hl::spiece_row(m, it, C::kCols, C::kML)) * sh.H + hh) * V + v0 +
+                                  hl::spiece_col(m, C::kCols) + 8);
+    CHECK(umax <= sh.B * sh.T * sh.H * V, "%s: u load past the tensor", what);
+    for (int p = 0; p < K * C::kCols / 4; ++p)
+      hmax = std::max(hmax, ((b * NT + c) * sh.H + hh) * K * V + (int64_t)hl::sout_row(p, C::kCols) * V + v0 +
+                                hl::sout_col(p, C::kCols) + 4);
+    CHECK(hmax <= sh.B * NT * sh.H * K * V, "%s: h store past the tensor", what);
+    for (int p = 0; p < 64 * C::kCols / 4; ++p)
+      vmax = std::max(vmax, ((b * sh.T + c * 64 + hl::sout_row(p, C::kCols)) * sh.H + hh) * V + v0 +
+                                hl::sout_col(p, C::kCols) + 4);
+    CHECK(vmax <= sh.B * sh.T * sh.H * V, "%s: v_new store past the tensor", what);
+    CHECK((63 * tok_k + K) * 2 < (INT64_C(1) << 32) && (63 * tok_v + V) * 2 < (INT64_C(1) << 32),
+          "%s: per-lane load offsets past 32 bits", what);
+  }
+  // Out buffers: state writes, memory reads, stores.
+  for (int rows : {K, 64}) {
+    if (rows == 64 && !DELTA) continue;
+    const char* which = rows == K ? "h" : "v_new";
+    Cover wr(rows, C::kCols);
+    for (int wq = 0; wq < NW; ++wq)
+      for (int blk = 0; blk < rows / 16; ++blk)
+        for (int r = 0; r < 4; ++r) {
+          uint32_t addr[64];
+          for (int lane = 0; lane < 64; ++lane) {
+            const int i = hl::sout_put(blk, r, lane, wq, C::kOutPitch);
+            wr.add(i / C::kOutPitch, i % C::kOutPitch, what);
+            CHECK(i % C::kOutPitch < C::kCols, "%s: %s write in the row pad", what, which);
+            addr[lane] = (uint32_t)i * 4;
+          }
+          check_banks(addr, 4, what, blk, r);
+        }
+    wr.exactly_once(what);
+    Cover rd(rows, C::kCols / 4);
+    const int pieces = rows * C::kCols / 4;
+    CHECK(pieces % C::kML == 0, "%s: %s pieces per memory lane", what, which);
+    for (int p = 0; p < pieces; ++p) {
+      const int row = hl::sout_row(p, C::kCols), col = hl::sout_col(p, C::kCols);
+      CHECK(col % 4 == 0 && (row * C::kOutPitch + col) % 4 == 0, "%s: %s block misaligned", what, which);
+      rd.add(row, col / 4, what);
+    }
+    rd.exactly_once(what);
+  }
+}
+
 // --------------------------------------------------------------------------- recompute_w_u
 
 // Logical (row, element) at byte `a` of an xtile_off tile.
@@ -599,6 +704,16 @@ int main() {
   H_ALL(64, 128, 5)
   H_ALL(64, 64, 5)
   check_h<128, 128, 1, 2, true, true, true>();  // the unsplit form
+  check_small<64, 64, 2, true>();
+  check_small<64, 64, 2, false>();
+  check_small<64, 128, 2, true>();
+  check_small<128, 64, 2, true>();
+  check_small<128, 128, 2, true>();
+  check_small<128, 128, 2, false>();
+  check_small<64, 64, 1, true>();
+  check_small<128, 128, 1, true>();
+  check_small<64, 64, 4, true>();
+  check_small<64, 128, 4, false>();
 #define F_ALL(K, V)                   \
   check_fused<K, V, true, true>();    \
   check_fused<K, V, true, false>();   \

@@ -2,7 +2,9 @@
 
 The bf16 chunk_fwd_h kernel and the fused h + o kernel copy chunk tiles
 global -> LDS with hand-built 32-bit lane offsets, read them back through an
-XOR swizzle and wait for them with hand-counted vmcnt values.  A slip there
+XOR swizzle and wait for them with hand-counted vmcnt values; the small-grid
+chunk_fwd_h kernel stages its tiles and hands h and v_new between its waves
+through LDS buffers whose layout it shares with the checker.  A slip there
 would fault the GPU or race rather than fail a numerical test, so
 tests/csrc/dma_check.cpp evaluates the very index functions and layout
 constants the kernels use (theorem_amd/csrc/h_layout.h, pipe_cfg.h) on the
@@ -95,6 +97,18 @@ MUTATIONS = [
     ("pipe_cfg.h", "static constexpr int kWaitSteady = kPf + kStores;",
      "static constexpr int kWaitSteady = kPf + kStores - 1;",
      "fused: steady-state wait one op too tight"),
+    ("h_layout.h", "THM_HD constexpr int spiece_row(int m, int it, int n, int ml) { return m / (n / 8) + it * (ml / (n / 8)); }",
+     "THM_HD constexpr int spiece_row(int m, int it, int n, int ml) { return m / (n / 8) + it * (ml / (n / 4)); }",
+     "small chunk_fwd_h: load pieces at the wrong row stride"),
+    ("h_layout.h", "  return (16 * blk + 4 * (lane >> 4) + r) * pitch + 16 * wq + (lane & 15);",
+     "  return (16 * blk + 4 * (lane >> 4) + r) * pitch + 16 * wq + (lane & 7);",
+     "small chunk_fwd_h: out-buffer column of half the lanes"),
+    ("h_layout.h", "THM_HD constexpr int sout_col(int p, int cols) { return 4 * (p % (cols / 4)); }",
+     "THM_HD constexpr int sout_col(int p, int cols) { return 4 * (p % (cols / 8)); }",
+     "small chunk_fwd_h: out-buffer pieces miss half the columns"),
+    ("pipe_cfg.h", "  static constexpr int kOutPitch = kCols + 4;",
+     "  static constexpr int kOutPitch = kCols;",
+     "small chunk_fwd_h: out-buffer rows unpadded (bank conflicts)"),
 ]
 
 

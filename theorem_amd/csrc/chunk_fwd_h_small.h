@@ -38,40 +38,13 @@
 
 #include "h_layout.h"
 #include "mfma.h"
+#include "pipe_cfg.h"
 #include "vmem.h"
 
 namespace thm {
 namespace {
 
-// NW state waves + NW memory waves per workgroup; the workgroup owns a V-tile
-// of 16 NW columns.
-template <int K, int NW, bool DELTA>
-struct SCfg {
-  static constexpr int kThreads = 128 * NW;
-  static constexpr int kCols = 16 * NW;                // V-tile width
-  static constexpr int kKPitch = K + 8;                // bf16 elements per k / w row (16-byte pad)
-  static constexpr int kUPitch = kCols + 8;            // bf16 elements per u / v row of the V-tile
-  static constexpr int kKTileB = 64 * kKPitch * 2;     // bytes
-  static constexpr int kUTileB = 64 * kUPitch * 2;
-  static constexpr int kGateB = 80 * 4;                // 64 factors e^{g_last - g_j}, e^{g_last}, pad
-  static constexpr int kStageB = kKTileB * (DELTA ? 2 : 1) + kUTileB + kGateB;
-  // Out buffers: fp32, row-major, kOutPitch floats per row.  The state waves
-  // write single floats, 16 lanes of a row-quad group 4 rows apart; a pitch of
-  // 4 mod 16 floats puts those 4 rows 16 banks apart (conflict-free).
-  static constexpr int kOutPitch = kCols + 4;
-  static constexpr int kHOutB = K * kOutPitch * 4;
-  static constexpr int kVOutB = DELTA ? 64 * kOutPitch * 4 : 0;
-  static constexpr int kLds = 2 * kStageB + 2 * (kHOutB + kVOutB);
-  // memory-wave loads per lane per chunk (16-byte pieces of 8 bf16)
-  static constexpr int kML = 64 * NW;                  // memory lanes
-  static constexpr int kKCPR = K / 8;                  // pieces per k / w row
-  static constexpr int kKLoads = 64 * kKCPR / kML;
-  static constexpr int kUCPR = kCols / 8;              // pieces per u row of the V-tile
-  static constexpr int kULoads = 64 * kUCPR / kML;
-  static_assert(NW == 1 || NW == 2 || NW == 4, "state waves");
-  static_assert(kStageB % 16 == 0 && kLds <= 160 * 1024, "LDS budget");
-  static_assert(64 * kKCPR % kML == 0 && kML % kKCPR == 0 && kML % kUCPR == 0, "load split");
-};
+using pipe::SCfg;
 
 template <int K, int V, int NW, bool DELTA, bool HAS_G>
 __global__ void __launch_bounds__(128 * NW)
@@ -119,9 +92,9 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
       for (int r = 0; r < 4; ++r) S[kb][r] = h0 ? h0[st_base + (16 * kb + 4 * grp + r) * V + vcol] : 0.f;
     // Rows 16 b + 4 grp + r of this lane's column of an out buffer.
     auto put_out = [&](char* buf, int blk, f32x4 v) {
-      float* const p = reinterpret_cast<float*>(buf) + (16 * blk + 4 * grp) * C::kOutPitch + ucol;
+      float* const p = reinterpret_cast<float*>(buf);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) p[r * C::kOutPitch] = v[r];
+      for (int r = 0; r < 4; ++r) p[hl::sout_put(blk, r, lane, wv, C::kOutPitch)] = v[r];
     };
     lds_barrier();  // B_0: chunk 0 staged
     for (int64_t c = 0; c < NT; ++c) {
@@ -209,11 +182,12 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
   // ------------------------------------------------------------------ memory waves
   const int m = wv - NW;
   const int tid = (int)threadIdx.x - C::kML;  // 0 .. kML - 1
-  // Loads: piece it of this lane is row kj0 + it * (kML / kKCPR), 8 elements
-  // from column kcol (k / w), or row uj0 + it * (kML / kUCPR), column ucol0 (u / v).
+  // Loads: piece it of this lane is row hl::spiece_row(tid, it, n, kML),
+  // elements hl::spiece_col(tid, n) .. + 7 of the k / w (n = K) or u / v
+  // (n = kCols) tile; successive pieces are kKRows / kURows rows apart.
   constexpr int kKRows = C::kML / C::kKCPR, kURows = C::kML / C::kUCPR;
-  const int kj0 = tid / C::kKCPR, kcol = (tid % C::kKCPR) * 8;
-  const int uj0 = tid / C::kUCPR, ucol0 = (tid % C::kUCPR) * 8;
+  const int kj0 = hl::spiece_row(tid, 0, K, C::kML), kcol = hl::spiece_col(tid, K);
+  const int uj0 = hl::spiece_row(tid, 0, C::kCols, C::kML), ucol0 = hl::spiece_col(tid, C::kCols);
   const uint32_t koff = (uint32_t)(kj0 * tok_k + kcol) * 2;        // bytes from the chunk base
   const uint32_t kstep = (uint32_t)(kKRows * tok_k) * 2;
   const uint32_t uoff = (uint32_t)(uj0 * tok_v + v0 + ucol0) * 2;
@@ -274,10 +248,10 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
       }
     }
   };
-  // h[c] and v_new[c] from out buffer s: piece p = i * kML + tid is row
-  // p / (4 NW), columns 4 (p % (4 NW)) .. + 3, read as one 16-byte LDS block
-  // and stored as 16 bytes of h or 8 of v_new.  All of a chunk's blocks are
-  // read before the first store.
+  // h[c] and v_new[c] from out buffer s: piece p = i * kML + tid (row
+  // hl::sout_row, columns hl::sout_col .. + 3) is read as one 16-byte LDS
+  // block and stored as 16 bytes of h or 8 of v_new.  All of a chunk's blocks
+  // are read before the first store.
   constexpr int kHPieces = K / 16, kVPieces = 4;  // per memory lane
   auto store_out = [&](int64_t c, int s) {
     const float* const ho = reinterpret_cast<const float*>(hob + s * C::kHOutB);
@@ -286,20 +260,20 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
 #pragma unroll
     for (int i = 0; i < kHPieces; ++i) {
       const int p = i * C::kML + tid;
-      hv[i] = *reinterpret_cast<const f32x4*>(ho + (p / (4 * NW)) * C::kOutPitch + 4 * (p % (4 * NW)));
+      hv[i] = *reinterpret_cast<const f32x4*>(ho + hl::sout_row(p, C::kCols) * C::kOutPitch + hl::sout_col(p, C::kCols));
     }
     if constexpr (DELTA) {
 #pragma unroll
       for (int i = 0; i < kVPieces; ++i) {
         const int p = i * C::kML + tid;
-        vv[i] = *reinterpret_cast<const f32x4*>(vo + (p / (4 * NW)) * C::kOutPitch + 4 * (p % (4 * NW)));
+        vv[i] = *reinterpret_cast<const f32x4*>(vo + hl::sout_row(p, C::kCols) * C::kOutPitch + hl::sout_col(p, C::kCols));
       }
     }
     float* const hb = hout + ((b * NT + c) * H + hh) * (int64_t)(K * V) + v0;
 #pragma unroll
     for (int i = 0; i < kHPieces; ++i) {
       const int p = i * C::kML + tid;
-      *reinterpret_cast<f32x4*>(hb + (p / (4 * NW)) * V + 4 * (p % (4 * NW))) = hv[i];
+      *reinterpret_cast<f32x4*>(hb + hl::sout_row(p, C::kCols) * V + hl::sout_col(p, C::kCols)) = hv[i];
     }
     if constexpr (DELTA) {
       if (vnew) {  // uniform
@@ -309,7 +283,7 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
           const int p = i * C::kML + tid;
           bf16x4 o;
           o[0] = (bf16)vv[i][0]; o[1] = (bf16)vv[i][1]; o[2] = (bf16)vv[i][2]; o[3] = (bf16)vv[i][3];
-          *reinterpret_cast<bf16x4*>(vb + (p / (4 * NW)) * tok_v + 4 * (p % (4 * NW))) = o;
+          *reinterpret_cast<bf16x4*>(vb + hl::sout_row(p, C::kCols) * tok_v + hl::sout_col(p, C::kCols)) = o;
         }
       }
     }

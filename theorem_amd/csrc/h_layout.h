@@ -187,5 +187,22 @@ THM_HD inline BhTile xcd_tile(int64_t blk, int64_t BH, int nvt) {
   return {blk / nvt, blk % nvt};
 }
 
+// Small-grid chunk_fwd_h kernel (chunk_fwd_h_small.h).  Memory lane m of ml
+// loads 8-element pieces of a [64 x n] bf16 tile (k, w: n = K; u: n = the
+// V-tile width): its piece it is row spiece_row(m, it, n, ml), elements
+// spiece_col(m, n) .. + 7.
+THM_HD constexpr int spiece_row(int m, int it, int n, int ml) { return m / (n / 8) + it * (ml / (n / 8)); }
+THM_HD constexpr int spiece_col(int m, int n) { return (m % (n / 8)) * 8; }
+// Out buffer (fp32, row-major, `pitch` floats per row): lane `lane` of state
+// wave wq writes rows 16 blk + 4 (lane / 16) + r (r = 0..3) of column
+// 16 wq + lane % 16, one float each.
+THM_HD constexpr int sout_put(int blk, int r, int lane, int wq, int pitch) {
+  return (16 * blk + 4 * (lane >> 4) + r) * pitch + 16 * wq + (lane & 15);
+}
+// Memory piece p of an out buffer of `cols` columns: row sout_row, columns
+// sout_col .. + 3 (one 16-byte block).
+THM_HD constexpr int sout_row(int p, int cols) { return p / (cols / 4); }
+THM_HD constexpr int sout_col(int p, int cols) { return 4 * (p % (cols / 4)); }
+
 }  // namespace hl
 }  // namespace thm
