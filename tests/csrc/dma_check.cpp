@@ -22,7 +22,11 @@
 //   * recompute_w_u's [k | v] tile and chunk_fwd_o's v, h and k tiles
 //     (padded, register-staged): the fragments hold the elements the products
 //     need and are read conflict-free; staging stores are bounded in
-//     conflicts.
+//     conflicts;
+//   * chunk_fwd_o's pipelined kernel: its walk (desc_walk_*) visits every tile
+//     once, in descending chunk order, and its load offsets (o_*_lane /
+//     o_*_step) read exactly the elements its staging writes, in bounds and
+//     in 32 bits up to the entry point's limit on H.
 // Exit status 0 and "dma_check: ok" on success; the first failures are printed.
 #include <algorithm>
 #include <cstdint>
@@ -680,6 +684,83 @@ static void check_row_tile(int n, const char* what) {
     }
 }
 
+// chunk_fwd_o's pipelined kernel: workgroup wg of G visits sequence indices
+// wg, wg + G, ... < B NT H, advancing a DescWalk by desc_walk_at(G).
+static void check_o_walk() {
+  struct Case {
+    uint32_t B, H, NT, G;
+  };
+  const Case cases[] = {{8, 16, 128, 512}, {2, 17, 32, 512}, {1, 1, 2, 1},     {3, 5, 7, 4},   {4, 64, 16, 512},
+                        {1, 260, 2, 512},  {2, 3, 5, 7},     {5, 1, 3, 2},     {8, 16, 128, 1024}, {7, 9, 11, 100}};
+  for (const Case& c : cases) {
+    const uint32_t tiles = c.B * c.NT * c.H;
+    std::vector<int> seen(tiles, 0);
+    const hl::DescWalk step = hl::desc_walk_at(c.G, c.B, c.H);
+    CHECK(step.b < c.B && step.hh < c.H, "o walk step (%u, %u, %u)", step.cq, step.b, step.hh);
+    for (uint32_t wg = 0; wg < std::min(c.G, tiles); ++wg) {
+      hl::DescWalk w = hl::desc_walk_at(wg, c.B, c.H);
+      for (uint32_t t = wg; t < tiles; t += c.G) {
+        const uint32_t bh = c.B * c.H, cq = t / bh, b = (t % bh) / c.H, hh = t % c.H;
+        CHECK(w.cq == cq && w.b == b && w.hh == hh, "o walk B=%u H=%u G=%u: t=%u at (%u,%u,%u), want (%u,%u,%u)", c.B,
+              c.H, c.G, t, w.cq, w.b, w.hh, cq, b, hh);
+        if (w.cq >= c.NT || w.b >= c.B || w.hh >= c.H) break;
+        const uint32_t tile = (w.b * c.NT + (c.NT - 1 - w.cq)) * c.H + w.hh;
+        ++seen[tile];
+        if (t + c.G < tiles) hl::desc_walk_step(w, step, c.B, c.H);
+      }
+    }
+    for (uint32_t tile = 0; tile < tiles; ++tile)
+      CHECK(seen[tile] == 1, "o walk B=%u H=%u NT=%u G=%u: tile %u visited %d times", c.B, c.H, c.NT, c.G, tile,
+            seen[tile]);
+  }
+}
+
+// chunk_fwd_o's pipelined loads: thread tid's load `it` of h, v and k lands on
+// the (row, element) its staging writes; q lane (i, grp) step s on token i,
+// elements 32 s + 8 grp.  Offsets are exact in 32 bits for H up to the entry
+// point's limit, 64 H max(K, V) 2 < 2^32.
+template <int K, int V>
+static void check_o_offsets() {
+  const int64_t h_max = ((INT64_C(1) << 32) - 1) / (64 * 2 * std::max(K, V));
+  for (int64_t H : {INT64_C(1), INT64_C(3), INT64_C(16), INT64_C(17), INT64_C(64), h_max}) {
+    std::vector<int> hcov(K * V / 4, 0);
+    for (int tid = 0; tid < 256; ++tid)
+      for (int it = 0; it < K * (V / 4) / 256; ++it) {
+        const int qi = tid + it * 256, r = qi / (V / 4), col = (qi % (V / 4)) * 4;
+        const int64_t off = (int64_t)hl::o_h_lane(tid, V) + hl::o_h_step(it, V);
+        CHECK(off % 16 == 0 && off / 4 == (int64_t)r * V + col && off + 16 <= (int64_t)K * V * 4,
+              "o h load K=%d V=%d tid %d it %d: offset %lld", K, V, tid, it, (long long)off);
+        if (off >= 0 && off / 16 < (int64_t)hcov.size()) ++hcov[off / 16];
+      }
+    for (size_t p = 0; p < hcov.size(); ++p) CHECK(hcov[p] == 1, "o h tile K=%d V=%d: 16 bytes %zu loaded %d times", K, V, p, hcov[p]);
+    for (int n : {K, V}) {
+      const int64_t row = H * n;
+      std::vector<int> cov(64 * n / 8, 0);
+      for (int tid = 0; tid < 256; ++tid)
+        for (int it = 0; it < 64 * (n / 8) / 256; ++it) {
+          const int qi = tid + it * 256, j = qi / (n / 8), col = (qi % (n / 8)) * 8;
+          const int64_t lane64 = ((int64_t)(tid / (n / 8)) * row + (tid % (n / 8)) * 8) * 2;
+          const uint32_t lane = hl::o_blk_lane(tid, n, row);
+          CHECK((int64_t)lane == lane64, "o block lane offset n=%d H=%lld tid %d overflows 32 bits", n, (long long)H, tid);
+          const int64_t off = lane64 + hl::o_blk_step(it, n, row);
+          CHECK(off % 16 == 0 && off / 2 == j * row + col && j < 64 && col + 8 <= n,
+                "o block load n=%d H=%lld tid %d it %d: offset %lld", n, (long long)H, tid, it, (long long)off);
+          if (j >= 0 && j < 64 && col >= 0 && col < n) ++cov[j * (n / 8) + col / 8];
+        }
+      for (size_t p = 0; p < cov.size(); ++p) CHECK(cov[p] == 1, "o block n=%d: piece %zu loaded %d times", n, p, cov[p]);
+    }
+    for (int i = 0; i < 64; ++i)
+      for (int grp = 0; grp < 4; ++grp)
+        for (int st = 0; st < K / 32; ++st) {
+          const int64_t lane64 = ((int64_t)i * H * K + 8 * grp) * 2;
+          CHECK((int64_t)hl::o_q_lane(i, grp, H * K) == lane64, "o q lane offset H=%lld i %d overflows", (long long)H, i);
+          const int64_t off = lane64 + 64 * st;
+          CHECK(off / 2 == (int64_t)i * H * K + 32 * st + 8 * grp && 32 * st + 8 * grp + 8 <= K, "o q load i %d grp %d s %d", i,
+                grp, st);
+        }
+  }
+}
+
 int main() {
   // Read patterns of both kernels: k / w / q rows (128 or 256 bytes), the u
   // V-tile (128 bytes) and the fused kernel's score tile P (128 bytes).
@@ -738,6 +819,11 @@ int main() {
     std::snprintf(what, sizeof what, "chunk_fwd_o k tile K=%d", V);
     check_row_tile(V, what);
   }
+  check_o_walk();
+  check_o_offsets<64, 64>();
+  check_o_offsets<64, 128>();
+  check_o_offsets<128, 64>();
+  check_o_offsets<128, 128>();
   if (g_fail) {
     std::fprintf(stderr, "dma_check: %d of %ld checks failed\n", g_fail, g_checks);
     return 1;

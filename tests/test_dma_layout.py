@@ -4,7 +4,9 @@ The bf16 chunk_fwd_h kernel and the fused h + o kernel copy chunk tiles
 global -> LDS with hand-built 32-bit lane offsets, read them back through an
 XOR swizzle and wait for them with hand-counted vmcnt values; the small-grid
 chunk_fwd_h kernel stages its tiles and hands h and v_new between its waves
-through LDS buffers whose layout it shares with the checker.  A slip there
+through LDS buffers whose layout it shares with the checker; chunk_fwd_o's
+pipelined kernel walks its tiles with carried coordinates and loads them with
+32-bit per-lane offsets.  A slip there
 would fault the GPU or race rather than fail a numerical test, so
 tests/csrc/dma_check.cpp evaluates the very index functions and layout
 constants the kernels use (theorem_amd/csrc/h_layout.h, pipe_cfg.h) on the
@@ -109,6 +111,14 @@ MUTATIONS = [
     ("pipe_cfg.h", "  static constexpr int kOutPitch = kCols + 4;",
      "  static constexpr int kOutPitch = kCols;",
      "small chunk_fwd_h: out-buffer rows unpadded (bank conflicts)"),
+    ("h_layout.h", "  if (w.b >= B) {", "  if (w.b > B) {",
+     "chunk_fwd_o walk: batch carry one late"),
+    ("h_layout.h", "  w.cq += step.cq;\n", "",
+     "chunk_fwd_o walk: whole-sweep part of the step dropped"),
+    ("h_layout.h", "(uint32_t)(tid % (n / 8)) * 8u) * 2u;", "(uint32_t)(tid % (n / 8)) * 4u) * 2u;",
+     "chunk_fwd_o: v / k lane offset at half the element stride"),
+    ("h_layout.h", "return (int64_t)it * (256 / (V / 4)) * V * 4; }", "return (int64_t)it * (256 / (V / 4)) * V * 2; }",
+     "chunk_fwd_o: h load step at half the row stride"),
 ]
 
 

@@ -195,7 +195,8 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
 // its compute, but nothing loads while it computes; at 3 resident workgroups
 // per CU that leaves HBM idle for a large part of each tile (the kernel with
 // its MFMA work removed runs in 60 % of the time).  Here each workgroup walks
-// tiles t, t + G, t + 2G, ... (G = 2 workgroups per CU) and issues the next
+// tiles t, t + G, t + 2G, ... of a sequence (G = 2 workgroups per CU; the
+// sequence takes the chunks in descending order) and issues the next
 // tile's global loads into registers before computing the current tile from
 // LDS, then stages them to LDS behind a barrier.  k is staged in LDS as well
 // (its fragments are plain 16-byte row reads), which keeps the prefetched set
@@ -238,46 +239,50 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   const int li = lane & 15;
   const int i = 16 * wv + li;  // this lane's query position
 
-  // Tile -> (b, c, head), head fastest (as the one-tile kernel).  The
-  // XCD-aware order of recompute_w_u (h_layout.h xcd_tile_order) would save
-  // ~1.5 % of this kernel's reads (g is the only per-token [B, T, H] array)
-  // but its division pushed this register-bound loop into spills.
-  auto tok_of = [&](int64_t t_, int64_t& hh, int64_t& tile) {
-    tile = t_;
-    const TileCoord tc = tile_coord(tile, H, NT, T);
-    hh = tc.hh;
-    return tc.tok0;
-  };
+  // Walk order (h_layout.h desc_walk_*): head fastest, chunks in descending
+  // order.  This kernel takes the same time in either order, but the kernel
+  // that runs after it does not: the next step's recompute_w_u (after the
+  // conv or directly after this kernel, with its own or shared k and g)
+  // takes 263-266 us instead of 271-278 at config 4, from the write-back of
+  // this kernel's output overlapping it in a different address order.  The
+  // walk advances with adds only: divisions in the loop pushed it into spills.
+  const uint32_t Hu = (uint32_t)H, Bu = (uint32_t)(tiles / (NT * H));
+  hl::DescWalk walk = hl::desc_walk_at(blockIdx.x, Bu, Hu);
+  const hl::DescWalk step = hl::desc_walk_at(gridDim.x, Bu, Hu);
   char* const lvb = reinterpret_cast<char*>(lv);
   char* const lhb = reinterpret_cast<char*>(lh);
   char* const lkb = reinterpret_cast<char*>(lk);
 
-  // Prefetched registers of one tile.
+  // Per-lane byte offsets of the tile's loads (the entry point checks
+  // 64 H max(K, V) 2 < 2^32), added to wave-uniform 64-bit bases.
+  const uint32_t h_off = hl::o_h_lane(tid, V);
+  const uint32_t v_off = hl::o_blk_lane(tid, V, H * V);
+  const uint32_t k_off = hl::o_blk_lane(tid, K, H * K);
+  const uint32_t q_off = hl::o_q_lane(i, grp, H * K);
+
+  // Prefetched registers of one tile, and its coordinates.
   u32x4 vr[C::kVLoads], hr[C::kHLoads], kr[C::kKLoads], qr[KS];
   float gr = 0.f;
-  auto prefetch = [&](int64_t t_) {
-    int64_t hh, tile;
-    const int64_t tok0 = tok_of(t_, hh, tile);
+  int64_t nx_hh = 0, nx_tok0 = 0;
+  auto prefetch = [&]() {  // the tile at `walk`
+    const int64_t c = (int64_t)NT - 1 - walk.cq;
+    const int64_t hh = walk.hh, tile = ((int64_t)walk.b * NT + c) * H + hh;
+    const int64_t tok0 = (int64_t)walk.b * T + c * 64;
+    nx_hh = hh;
+    nx_tok0 = tok0;
+    const char* const hb = reinterpret_cast<const char*>(hs + tile * (int64_t)(K * V));
+    const char* const vb = reinterpret_cast<const char*>(v + (tok0 * H + hh) * V);
+    const char* const kb = reinterpret_cast<const char*>(k + (tok0 * H + hh) * K);
+    const char* const qb = reinterpret_cast<const char*>(q + (tok0 * H + hh) * K);
+    static_assert(kOThreads == 256, "h_layout.h o_* offsets assume 256 threads");
 #pragma unroll
-    for (int it = 0; it < C::kHLoads; ++it) {
-      const int qi = tid + it * kOThreads;
-      const int r = qi / (V / 4), col = (qi - r * (V / 4)) * 4;
-      hr[it] = ldg16_nt(hs + tile * (int64_t)(K * V) + r * V + col);
-    }
+    for (int it = 0; it < C::kHLoads; ++it) hr[it] = ldg16_nt(hb + hl::o_h_step(it, V) + h_off);
 #pragma unroll
-    for (int it = 0; it < C::kVLoads; ++it) {
-      const int qi = tid + it * kOThreads;
-      const int j = qi / (V / 8), col = (qi - j * (V / 8)) * 8;
-      vr[it] = ldg16_nt(v + ((tok0 + j) * H + hh) * V + col);
-    }
+    for (int it = 0; it < C::kVLoads; ++it) vr[it] = ldg16_nt(vb + hl::o_blk_step(it, V, H * V) + v_off);
 #pragma unroll
-    for (int it = 0; it < C::kKLoads; ++it) {
-      const int qi = tid + it * kOThreads;
-      const int j = qi / (K / 8), col = (qi - j * (K / 8)) * 8;
-      kr[it] = ldg16_nt(k + ((tok0 + j) * H + hh) * K + col);
-    }
+    for (int it = 0; it < C::kKLoads; ++it) kr[it] = ldg16_nt(kb + hl::o_blk_step(it, K, H * K) + k_off);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qr[s] = ldg16_nt(q + ((tok0 + i) * H + hh) * K + 32 * s + 8 * grp);
+    for (int s = 0; s < KS; ++s) qr[s] = ldg16_nt(qb + 64 * s + q_off);
     gr = (tid < kBT && g) ? g[(tok0 + tid) * H + hh] : 0.f;
   };
   auto stage = [&]() {
@@ -306,7 +311,7 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 
   int64_t t = blockIdx.x;
   if (t >= tiles) return;  // whole workgroup
-  prefetch(t);
+  prefetch();
   stage();
   lds_barrier();
   for (;;) {
@@ -314,10 +319,12 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 #pragma unroll
     for (int s = 0; s < KS; ++s) qh[s] = __builtin_bit_cast(bf16x8, qr[s]);
     const int64_t tn = t + gridDim.x;
-    if (tn < tiles) prefetch(tn);  // in flight while tile t computes
+    const int64_t hh = nx_hh, tok0 = nx_tok0;  // tile t
+    if (tn < tiles) {  // in flight while tile t computes
+      hl::desc_walk_step(walk, step, Bu, Hu);
+      prefetch();
+    }
 
-    int64_t hh, tile;
-    const int64_t tok0 = tok_of(t, hh, tile);
     // Inter-chunk term, scaled by e^{g_i}.
     f32x4 acc[NB];
 #pragma unroll
@@ -644,6 +651,8 @@ extern "C" int thm_chunk_fwd_o(const void* q, const void* k, const void* v, cons
   if (g && ((uintptr_t)g % 4)) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
   if (!launch_fits(B * (T / kBT) * H, kOThreads)) return THM_ERR_BAD_SHAPE;
+  // 32-bit per-lane offsets of the pipelined kernel: 64 tokens x H heads.
+  if (kBT * H * (K > V ? K : V) * 2 >= (INT64_C(1) << 32)) return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = (qkv_dtype == THM_DTYPE_F32)
                      ? dispatch_o<float>(K, V, q, k, v, g, h, o, scale, B, T, H, s)

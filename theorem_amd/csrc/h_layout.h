@@ -204,5 +204,54 @@ THM_HD constexpr int sout_put(int blk, int r, int lane, int wq, int pitch) {
 THM_HD constexpr int sout_row(int p, int cols) { return p / (cols / 4); }
 THM_HD constexpr int sout_col(int p, int cols) { return 4 * (p % (cols / 4)); }
 
+// chunk_fwd_o's pipelined kernel.
+//
+// Walk: sequence index t = cq (B H) + b H + hh visits tile (b, chunk
+// NT - 1 - cq, head hh): head fastest, chunks in descending order.  A
+// workgroup starts at t = its index and steps by the grid size G; the step
+// is desc_walk_at(G) added with carries, so the loop has no division.
+struct DescWalk {
+  uint32_t cq, b, hh;
+};
+THM_HD inline DescWalk desc_walk_at(uint32_t t, uint32_t B, uint32_t H) {
+  const uint32_t bh = B * H, cq = t / bh, r = t - cq * bh, b = r / H;
+  return {cq, b, r - b * H};
+}
+// w += step (step.b < B and step.hh < H, as desc_walk_at gives).
+THM_HD inline void desc_walk_step(DescWalk& w, const DescWalk& step, uint32_t B, uint32_t H) {
+  w.hh += step.hh;
+  w.b += step.b;
+  w.cq += step.cq;
+  if (w.hh >= H) {
+    w.hh -= H;
+    ++w.b;
+  }
+  if (w.b >= B) {
+    w.b -= B;
+    ++w.cq;
+  }
+}
+// Loads of one tile, byte offsets = a per-lane part (loop-invariant, 32-bit)
+// plus a wave-uniform step per load `it` (256 threads):
+//   h [K x V] fp32: thread tid's load it is row tid / (V / 4) + it 256 / (V / 4),
+//     elements 4 (tid % (V / 4)) .. + 3;
+//   a [64 x n] bf16 token block (v: n = V, k: n = K; tokens `row_elems`
+//     elements apart): token tid / (n / 8) + it 256 / (n / 8), elements
+//     8 (tid % (n / 8)) .. + 7;
+//   q: lane (i, grp) reads token i, elements 32 s + 8 grp .. + 7 (step 64 s bytes).
+THM_HD constexpr uint32_t o_h_lane(int tid, int V) {
+  return ((uint32_t)(tid / (V / 4)) * (uint32_t)V + (uint32_t)(tid % (V / 4)) * 4u) * 4u;
+}
+THM_HD constexpr int64_t o_h_step(int it, int V) { return (int64_t)it * (256 / (V / 4)) * V * 4; }
+THM_HD constexpr uint32_t o_blk_lane(int tid, int n, int64_t row_elems) {
+  return ((uint32_t)(tid / (n / 8)) * (uint32_t)row_elems + (uint32_t)(tid % (n / 8)) * 8u) * 2u;
+}
+THM_HD constexpr int64_t o_blk_step(int it, int n, int64_t row_elems) {
+  return (int64_t)it * (256 / (n / 8)) * row_elems * 2;
+}
+THM_HD constexpr uint32_t o_q_lane(int i, int grp, int64_t row_elems) {
+  return ((uint32_t)i * (uint32_t)row_elems + 8u * (uint32_t)grp) * 2u;
+}
+
 }  // namespace hl
 }  // namespace thm
