@@ -23,6 +23,8 @@
 //     (padded, register-staged): the fragments hold the elements the products
 //     need and are read conflict-free; staging stores are bounded in
 //     conflicts;
+//   * the fused WY kernel's [k | v] tile (nat_row order): staging, transposed
+//     reads (conflict-free) and form_L's row reads (at most 2-way);
 //   * chunk_fwd_o's pipelined kernel: its walk (desc_walk_*) visits every tile
 //     once, in descending chunk order, and its load offsets (o_*_lane /
 //     o_*_step) read exactly the elements its staging writes, in bounds and
@@ -684,6 +686,33 @@ static void check_row_tile(int n, const char* what) {
     }
 }
 
+// The fused WY kernel's [k | v] tile (nat_row order at wy_tile_pitch): form_L
+// reads 16-byte k fragments of rows r0 + li (r0 a multiple of 16), elements
+// e0 + 8 grp; they land on the right elements and are at most 2-way
+// conflicted per 16-lane pass (rows r and r + 8 share a 256-byte window).
+static void check_nat_row_reads(int n, int kcols, const char* what) {
+  const int pitch = hl::wy_tile_pitch(n);
+  for (int r0 = 0; r0 < 64; r0 += 16)
+    for (int e0 = 0; e0 < kcols; e0 += 32) {
+      uint32_t addr[64];
+      for (int lane = 0; lane < 64; ++lane) {
+        addr[lane] = hl::ntile_off(r0 + (lane & 15), e0 + 8 * (lane >> 4), pitch);
+        CHECK(addr[lane] % 16 == 0, "%s: row read lane %d misaligned", what, lane);
+        for (int i = 0; i < 8; ++i) {
+          const auto d = pdecode(addr[lane] + 2 * i, pitch, n, true);
+          CHECK(d.first == r0 + (lane & 15) && d.second == e0 + 8 * (lane >> 4) + i, "%s: lane %d element %d", what,
+                lane, i);
+        }
+      }
+      for (int p = 0; p < 4; ++p) {
+        int cnt[64] = {0}, ways = 0;
+        for (int l = 16 * p; l < 16 * p + 16; ++l)
+          for (int d = 0; d < 4; ++d) ways = std::max(ways, ++cnt[(addr[l] / 4 + d) % 64]);
+        CHECK(ways <= 2, "%s: row-read pass %d at (%d, %d) is %d-way conflicted", what, p, r0, e0, ways);
+      }
+    }
+}
+
 // chunk_fwd_o's pipelined kernel: workgroup wg of G visits sequence indices
 // wg, wg + G, ... < B NT H, advancing a DescWalk by desc_walk_at(G).
 static void check_o_walk() {
@@ -819,6 +848,14 @@ int main() {
     std::snprintf(what, sizeof what, "chunk_fwd_o k tile K=%d", V);
     check_row_tile(V, what);
   }
+  for (int K : {64, 128})
+    for (int V : {64, 128}) {
+      char what[80];
+      std::snprintf(what, sizeof what, "fused WY [k | v] tile K=%d V=%d", K, V);
+      // 384-byte rows (K + V = 192): a staging pass spans two rows, 2-way.
+      check_padded(64, K + V, hl::wy_tile_pitch(K + V), true, {8}, K + V == 192 ? 2 : 1, what);
+      check_nat_row_reads(K + V, K, what);
+    }
   check_o_walk();
   check_o_offsets<64, 64>();
   check_o_offsets<64, 128>();

@@ -111,6 +111,9 @@ MUTATIONS = [
     ("pipe_cfg.h", "  static constexpr int kOutPitch = kCols + 4;",
      "  static constexpr int kOutPitch = kCols;",
      "small chunk_fwd_h: out-buffer rows unpadded (bank conflicts)"),
+    ("h_layout.h", "THM_HD constexpr int wy_tile_pitch(int n) { return tr_pitch(2 * n); }",
+     "THM_HD constexpr int wy_tile_pitch(int n) { return 2 * n + 16; }",
+     "fused WY tile: 16-byte row pad (conflicts in the transposed reads)"),
     ("h_layout.h", "  if (w.b >= B) {", "  if (w.b > B) {",
      "chunk_fwd_o walk: batch carry one late"),
     ("h_layout.h", "  w.cq += step.cq;\n", "",

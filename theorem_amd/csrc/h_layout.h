@@ -133,6 +133,12 @@ THM_HD constexpr uint32_t xtr_frag_off(int k0, int half, int c0, int lane, int r
 //     each of 16 consecutive rows per pass: conflict-free when pitch / 16 is
 //     odd: row_pitch.
 THM_HD constexpr int tr_pitch(int row_bytes) { return row_bytes + 32; }
+// The fused WY kernel's [k | v] tile (64 rows of n = K + V bf16): natural-order
+// transposed reads in its products, 16-byte row reads (form_L's k fragments)
+// of 16 consecutive rows, so the natural-order layout above: 2-way conflicts
+// for the row reads (rows r and r + 8 share a bank window), none for the
+// transposed ones, which are four times as many.
+THM_HD constexpr int wy_tile_pitch(int n) { return tr_pitch(2 * n); }
 THM_HD constexpr int row_pitch(int row_bytes) { return row_bytes + 16; }
 THM_HD constexpr int nat_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 // Element e of row r: plain (paired-order and row-read tiles) and with the

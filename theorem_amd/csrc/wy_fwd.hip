@@ -23,6 +23,7 @@
 // recompute_w_u's, so w and u equal the two-kernel path's bit for bit.
 // bf16 inputs only.  HBM traffic per tile: k, v, beta, g read once, w, u
 // written once.
+#include "h_layout.h"
 #include "wy_blocks.h"
 
 namespace thm {
@@ -37,8 +38,10 @@ constexpr int kWyThreads = 256;
 template <int K, int V>
 struct WyCfg {
   static constexpr int kN = K + V;
-  static constexpr int kPitch = kN + 8;  // [k | v] tile row pitch, bf16 elements (16-byte pad)
-  static constexpr int kTileBytes = kBT * kPitch * 2;
+  // [k | v] tile: row pitch in bytes, rows stored in the nat_row order
+  // (h_layout.h wy_tile_pitch, ntile_off, ntr_frag_off).
+  static constexpr int kPitch = hl::wy_tile_pitch(kN);
+  static constexpr int kTileBytes = kBT * kPitch;
   static constexpr int kInvBytes = wy::kLdsFloats * 4;
   static constexpr int kUnion = kTileBytes > kInvBytes ? kTileBytes : kInvBytes;
   static constexpr int kNB = kN / 16;
@@ -77,11 +80,12 @@ __device__ __forceinline__ WyOperands wy_operands(const float* Xb, const float* 
 }
 
 // D[n][t] = sum_j X[j][n] A'[t][j] for this wave's 16 tokens, stored to w / u:
-// the [k | v] tile xs (row pitch `pitch` bf16) gives the X^T fragments by
-// ds_read_b64_tr_b16; each lane ends with features 16 nb + 4 grp .. + 3 of
-// token t = 16 wv + li, one 8-byte store.  The products are recompute_w_u's.
+// the [k | v] tile xs (`pitch` bytes per row, rows in the nat_row order) gives
+// the X^T fragments by ds_read_b64_tr_b16 in the natural order; each lane
+// ends with features 16 nb + 4 grp .. + 3 of token t = 16 wv + li, one 8-byte
+// store.  The products are recompute_w_u's.
 template <int K, int V>
-__device__ __forceinline__ void wy_products(const bf16* xs, int pitch, const WyOperands& op, bf16* w, bf16* u,
+__device__ __forceinline__ void wy_products(const char* xs, int pitch, const WyOperands& op, bf16* w, bf16* u,
                                             int64_t trow) {
   const int lane = lane_id(), grp = lane >> 4;
 #pragma unroll
@@ -90,8 +94,9 @@ __device__ __forceinline__ void wy_products(const bf16* xs, int pitch, const WyO
     f32x4 acc = zero4();
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int r0 = tr_row_natural(32 * s, 0), r1 = tr_row_natural(32 * s, 1);
-      const bf16x8 xh = frag_tr(xs, pitch, r0, r1, 16 * nb);
+      const bf16x8 xh =
+          concat(ds_read_tr16(reinterpret_cast<const bf16*>(xs + hl::ntr_frag_off(32 * s, 0, 16 * nb, lane, pitch))),
+                 ds_read_tr16(reinterpret_cast<const bf16*>(xs + hl::ntr_frag_off(32 * s, 1, 16 * nb, lane, pitch))));
       acc = mfma16x16x32(xh, is_w ? op.awh[s] : op.auh[s], acc);
       acc = mfma16x16x32(xh, is_w ? op.awl[s] : op.aul[s], acc);
     }
@@ -113,7 +118,7 @@ wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
   float* const Lb = reinterpret_cast<float*>(lds);  // L = sign M, lower blocks
   float* const Xb = Lb + 10 * kBlk;                  // X = A_c, lower blocks
   float* const Tb = Xb + 10 * kBlk;                  // per-level partial products
-  bf16* const xs = reinterpret_cast<bf16*>(lds);    // [k | v] tile, after the inversion
+  char* const xs = lds;                              // [k | v] tile, after the inversion
 
   const TileCoord tc = tile_coord(blockIdx.x, H, NT, T);
   const int64_t h = tc.hh;
@@ -164,7 +169,7 @@ wy_fwd_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
     const int q = tid + it * kWyThreads;
     const int j = q / C::kCPR;
     const int col = (q - j * C::kCPR) * 8;
-    *reinterpret_cast<u32x4*>(xs + j * C::kPitch + col) = xr[it];
+    *reinterpret_cast<u32x4*>(xs + hl::ntile_off(j, col, C::kPitch)) = xr[it];
   }
   lds_barrier();
 
@@ -196,7 +201,7 @@ wy_fwd_pipe_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
                    bf16* __restrict__ u, int64_t T, int64_t H, int64_t NT, int64_t tiles) {
   using C = WyCfg<K, V>;
   constexpr int KS = C::KS;
-  __shared__ __attribute__((aligned(16))) bf16 xs[kBT * C::kPitch];  // [k | v] tile
+  __shared__ __attribute__((aligned(16))) char xs[kBT * C::kPitch];  // [k | v] tile
   __shared__ float Lb[10 * kBlk];  // L = sign M, lower blocks
   __shared__ float Xb[10 * kBlk];  // X = A_c, lower blocks
   __shared__ float Tb[3 * kBlk];   // per-level partial products
@@ -240,7 +245,7 @@ wy_fwd_pipe_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
       const int q = tid + it * kWyThreads;
       const int j = q / C::kCPR;
       const int col = (q - j * C::kCPR) * 8;
-      *reinterpret_cast<u32x4*>(xs + j * C::kPitch + col) = xr[it];
+      *reinterpret_cast<u32x4*>(xs + hl::ntile_off(j, col, C::kPitch)) = xr[it];
     }
     if (tid < kBT) {
       sb[tid] = br;
@@ -264,7 +269,8 @@ wy_fwd_pipe_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-      for (int s = 0; s < KS; ++s) fh[tb][s] = load8(xs + (16 * tb + li) * C::kPitch + 32 * s + 8 * grp);
+      for (int s = 0; s < KS; ++s)
+        fh[tb][s] = load8(reinterpret_cast<const bf16*>(xs + hl::ntile_off(16 * tb + li, 32 * s + 8 * grp, C::kPitch)));
     wy::form_L<SIGN, KS, false>(fh, fl, sb, sg, Lb, wv);
     lds_barrier();
     wy::invert_L(Lb, Xb, Tb, wv);  // ends with a barrier
