@@ -219,20 +219,24 @@ wy_fwd_pipe_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
     return tc.tok0;
   };
 
-  // Prefetched registers of one tile (thread q: row q / kCPR, 16-byte chunk q % kCPR).
+  // Prefetched registers of one tile: the k block, then the v block, each
+  // loaded as in chunk_fwd_o (h_layout.h o_blk_lane / o_blk_step: a 32-bit
+  // per-lane offset on a wave-uniform base; thread tid's load it is token
+  // tid / (n / 8) + it 256 / (n / 8), elements 8 (tid % (n / 8)) .. + 7).
+  constexpr int kLK = K / 32, kLV = V / 32;
+  static_assert(kLK + kLV == C::kLoads && kWyThreads == 256, "load split");
+  const uint32_t k_off = hl::o_blk_lane(tid, K, H * K), v_off = hl::o_blk_lane(tid, V, H * V);
   u32x4 xr[C::kLoads];
   float br = 0.f, gr = 0.f;
   auto prefetch = [&](int64_t tile) {
     int64_t h;
     const int64_t tok0 = tok_of(tile, h);
+    const char* const kb = reinterpret_cast<const char*>(k + (tok0 * H + h) * K);
+    const char* const vb = reinterpret_cast<const char*>(v + (tok0 * H + h) * V);
 #pragma unroll
-    for (int it = 0; it < C::kLoads; ++it) {
-      const int q = tid + it * kWyThreads;
-      const int j = q / C::kCPR;
-      const int col = (q - j * C::kCPR) * 8;
-      const int64_t row = (tok0 + j) * H + h;
-      xr[it] = ldg16_nt(col < K ? (const void*)(k + row * K + col) : (const void*)(v + row * V + (col - K)));
-    }
+    for (int it = 0; it < kLK; ++it) xr[it] = ldg16_nt(kb + hl::o_blk_step(it, K, H * K) + k_off);
+#pragma unroll
+    for (int it = 0; it < kLV; ++it) xr[kLK + it] = ldg16_nt(vb + hl::o_blk_step(it, V, H * V) + v_off);
     if (tid < kBT) {
       const int64_t row = (tok0 + tid) * H + h;
       br = beta[row];
@@ -241,11 +245,14 @@ wy_fwd_pipe_kernel(const bf16* __restrict__ k, const bf16* __restrict__ v,
   };
   auto stage = [&]() {
 #pragma unroll
-    for (int it = 0; it < C::kLoads; ++it) {
-      const int q = tid + it * kWyThreads;
-      const int j = q / C::kCPR;
-      const int col = (q - j * C::kCPR) * 8;
+    for (int it = 0; it < kLK; ++it) {
+      const int q = tid + it * kWyThreads, j = q / (K / 8), col = (q % (K / 8)) * 8;
       *reinterpret_cast<u32x4*>(xs + hl::ntile_off(j, col, C::kPitch)) = xr[it];
+    }
+#pragma unroll
+    for (int it = 0; it < kLV; ++it) {
+      const int q = tid + it * kWyThreads, j = q / (V / 8), col = (q % (V / 8)) * 8;
+      *reinterpret_cast<u32x4*>(xs + hl::ntile_off(j, K + col, C::kPitch)) = xr[kLK + it];
     }
     if (tid < kBT) {
       sb[tid] = br;
@@ -330,6 +337,8 @@ extern "C" int thm_wy_fwd(const void* k, const void* v, const void* beta, const 
   if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
   if (!launch_fits(B * (T / kBT) * H, kWyThreads)) return THM_ERR_BAD_SHAPE;
+  // 32-bit per-lane offsets of the pipelined kernel's loads: 64 tokens x H heads.
+  if (kBT * H * (K > V ? K : V) * 2 >= (INT64_C(1) << 32)) return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (K == 64 && V == 64) e = launch_wy<64, 64>(k, v, beta, g, w, u, B, T, H, sign, s);
