@@ -27,6 +27,7 @@
 // HBM traffic per tile: k, beta, g read once, A written once.
 #include <type_traits>
 
+#include "h_layout.h"
 #include "wy_blocks.h"
 
 namespace thm {
@@ -118,11 +119,13 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
 // loads are in flight through form_L and the inversion; the k tile is staged
 // in LDS and the MFMA fragments are read from there.  The arithmetic is the
 // one-tile kernel's, so A is bit-identical.
-// Workgroups per CU: 3 for K = 64 (137 VGPRs); for K = 128 the 168-register
-// cap of 3 made the compiler spill, and 2 measured faster (149 against 153 us
-// at config 4; K = 64: 107 us at 3 against 135 at 2).
+// Workgroups per CU: 3.  The k loads go through one 32-bit per-lane offset on
+// a wave-uniform base (h_layout.h o_blk_lane / o_blk_step), which brings the
+// K = 128 form to 159 VGPRs, under the 168-register cap of 3 workgroups
+// (with 64-bit addresses per load it spilled there, and ran at 2): config 4
+// 140 -> 116 us, A bit-identical.  K = 64: 107 us at 3 against 135 at 2.
 template <int K>
-constexpr int ab_pipe_wgs_per_cu() { return K == 128 ? 2 : 3; }
+constexpr int ab_pipe_wgs_per_cu() { return 3; }
 
 template <int K, int SIGN>
 __global__ void __launch_bounds__(kABThreads, ab_pipe_wgs_per_cu<K>())
@@ -152,15 +155,13 @@ wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ bet
   };
   u32x4 kr[kLoads];
   float br = 0.f, gr = 0.f;
+  const uint32_t k_off = hl::o_blk_lane(tid, K, H * K);
   auto prefetch = [&](int64_t tile) {
     int64_t h;
     const int64_t tok0 = tok_of(tile, h);
+    const char* const kb = reinterpret_cast<const char*>(k + (tok0 * H + h) * K);
 #pragma unroll
-    for (int it = 0; it < kLoads; ++it) {
-      const int q = tid + it * kABThreads;
-      const int j = q / kCPR, col = (q - j * kCPR) * 8;
-      kr[it] = ldg16_nt(k + ((tok0 + j) * H + h) * K + col);
-    }
+    for (int it = 0; it < kLoads; ++it) kr[it] = ldg16_nt(kb + hl::o_blk_step(it, K, H * K) + k_off);
     if (tid < kBT) {
       const int64_t row = (tok0 + tid) * H + h;
       br = beta[row];
@@ -253,6 +254,8 @@ extern "C" int thm_wy_build_A(const void* k, const void* beta, const void* g, vo
   if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
   if (!launch_fits(B * (T / kBT) * H, kABThreads)) return THM_ERR_BAD_SHAPE;
+  // 32-bit per-lane offsets of the pipelined kernel's k loads: 64 tokens x H heads.
+  if (kBT * H * K * 2 >= (INT64_C(1) << 32)) return THM_ERR_BAD_SHAPE;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (k_dtype == THM_DTYPE_F32)
