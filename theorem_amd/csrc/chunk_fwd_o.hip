@@ -206,7 +206,7 @@ constexpr int kOPipeWGsPerCU = 2;
 template <int K, int V>
 struct OPCfg {
   static constexpr int kPitchB = hl::tr_pitch(V * 2);    // bytes per v / h row (layouts as in OCfg)
-  static constexpr int kKPitchB = hl::row_pitch(K * 2);  // bytes per k row (16-byte row reads)
+  static constexpr int kKPitchB = hl::tr_pitch(K * 2);  // bytes per k row (16-byte row reads)
   static constexpr int kVTile = kBT * kPitchB / 2;       // bf16 elements
   static constexpr int kHTile = K * kPitchB / 2;
   static constexpr int kKTile = kBT * kKPitchB / 2;

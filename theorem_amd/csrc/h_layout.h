@@ -129,17 +129,17 @@ THM_HD constexpr uint32_t xtr_frag_off(int k0, int half, int c0, int lane, int r
 //     r0 .. r0 + 3 and r0 + 8 .. r0 + 11, which no linear pitch separates, so
 //     natural-order tiles store logical row r at physical row nat_row(r) (bits
 //     2 and 3 of r swapped): each pass then reads 8 consecutive physical rows.
-//   * 16-byte row reads (and 8-byte paired-order row reads) take 16 bytes from
-//     each of 16 consecutive rows per pass: conflict-free when pitch / 16 is
-//     odd: row_pitch.
+//   * 16-byte row reads of 16 consecutive rows (chunk_fwd_o's k fragments)
+//     are served 32 lanes at a time over 128 banks (512 bytes), as measured
+//     on gfx950: two column groups of 16 rows per pass, which a pitch of
+//     row_bytes + 32 spreads over distinct banks (a 16-byte pad left 0.11
+//     conflict cycles per access).
 THM_HD constexpr int tr_pitch(int row_bytes) { return row_bytes + 32; }
 // The fused WY kernel's [k | v] tile (64 rows of n = K + V bf16): natural-order
-// transposed reads in its products, 16-byte row reads (form_L's k fragments)
-// of 16 consecutive rows, so the natural-order layout above: 2-way conflicts
-// for the row reads (rows r and r + 8 share a bank window), none for the
-// transposed ones, which are four times as many.
+// transposed reads in its products and 16-byte row reads (form_L's k
+// fragments) of 16 consecutive rows, so the natural-order layout above, which
+// serves both without bank conflicts.
 THM_HD constexpr int wy_tile_pitch(int n) { return tr_pitch(2 * n); }
-THM_HD constexpr int row_pitch(int row_bytes) { return row_bytes + 16; }
 THM_HD constexpr int nat_row(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 // Element e of row r: plain (paired-order and row-read tiles) and with the
 // natural-order row permutation.

@@ -133,7 +133,9 @@ wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ bet
                        const float* __restrict__ g, float* __restrict__ A, int64_t T, int64_t H,
                        int64_t NT, int64_t tiles) {
   constexpr int KS = K / 32;
-  constexpr int kPitch = K + 8;                       // bf16 elements (16-byte pad)
+  // bf16 elements per k row: a 32-byte pad (h_layout.h tr_pitch), under which
+  // the 16-byte fragment reads of 16 rows are conflict-free on gfx950.
+  constexpr int kPitch = hl::tr_pitch(2 * K) / 2;
   constexpr int kCPR = K / 8;                         // 16-byte chunks per k row
   constexpr int kLoads = kBT * kCPR / kABThreads;     // per thread
   static_assert(kBT * kCPR % kABThreads == 0, "staging split");
