@@ -733,6 +733,35 @@ static void check_nat_row_reads(int n, int kcols, const char* what) {
     }
 }
 
+// The XCD-aware tile order of recompute_w_u and the A-builder: a bijection of
+// [0, BNT H); when BNT is a multiple of 8 the H heads of one (b, chunk) get
+// launch indices of one residue mod 8 (one XCD).
+static void check_xcd_tile_order() {
+  for (int64_t H : {1, 3, 8, 16, 17, 64})
+    for (int64_t BNT : {1, 7, 8, 16, 24, 256}) {
+      const uint32_t n = (uint32_t)(BNT * H);
+      std::vector<int> seen(n, 0);
+      std::vector<int> xcd_of(BNT, -1);
+      for (uint32_t t = 0; t < n; ++t) {
+        const uint32_t tile = hl::xcd_tile_order(t, H, BNT);
+        if (tile >= n) {
+          CHECK(false, "xcd_tile_order(%u, H=%lld, BNT=%lld) = %u out of range", t, (long long)H, (long long)BNT, tile);
+          continue;
+        }
+        ++seen[tile];
+        if (BNT % 8 == 0) {
+          const int64_t bc = tile / H;
+          if (xcd_of[bc] < 0) xcd_of[bc] = (int)(t % 8);
+          CHECK(xcd_of[bc] == (int)(t % 8), "xcd_tile_order H=%lld BNT=%lld: heads of (b, chunk) %lld on two XCDs",
+                (long long)H, (long long)BNT, (long long)bc);
+        }
+      }
+      for (uint32_t i = 0; i < n; ++i)
+        CHECK(seen[i] == 1, "xcd_tile_order H=%lld BNT=%lld: tile %u taken %d times", (long long)H, (long long)BNT, i,
+              seen[i]);
+    }
+}
+
 // chunk_fwd_o's pipelined kernel: workgroup wg of G visits sequence indices
 // wg, wg + G, ... < B NT H, advancing a DescWalk by desc_walk_at(G).
 static void check_o_walk() {
@@ -876,6 +905,7 @@ int main() {
       check_padded(64, K + V, hl::wy_tile_pitch(K + V), true, {8}, K + V == 192 ? 2 : 1, what);
       check_nat_row_reads(K + V, K, what);
     }
+  check_xcd_tile_order();
   check_o_walk();
   check_o_offsets<64, 64>();
   check_o_offsets<64, 128>();

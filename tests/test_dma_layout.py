@@ -114,6 +114,9 @@ MUTATIONS = [
     ("h_layout.h", "THM_HD constexpr int wy_tile_pitch(int n) { return tr_pitch(2 * n); }",
      "THM_HD constexpr int wy_tile_pitch(int n) { return 2 * n + 16; }",
      "fused WY tile: 16-byte row pad (conflicts in the transposed reads)"),
+    ("h_layout.h", "  return (sq * 8u + (t & 7u)) * h + (slot - sq * h);",
+     "  return (sq * 8u + (t & 7u)) * h + (slot - sq * h) / 2;",
+     "xcd_tile_order: head index halved (not a bijection)"),
     ("h_layout.h", "  if (w.b >= B) {", "  if (w.b > B) {",
      "chunk_fwd_o walk: batch carry one late"),
     ("h_layout.h", "  w.cq += step.cq;\n", "",
