@@ -177,11 +177,7 @@ static void check_read(ReadKind kind, int r0, int c0, int rb, const char* what) 
       }
     }
   }
-  // The fused kernel's score fragments (16-byte rows of its swizzled q and k
-  // stages) are 2-way conflicted under the measured 16-byte model: the swizzle
-  // serves its 8-byte paired and transposed reads, and the scores are off the
-  // chunk's critical path (the output waves wait for the state waves there).
-  check_banks(addr, bytes, what, r0, c0, kind == kRow8 ? 2 : 1);
+  check_banks(addr, bytes, what, r0, c0);
 }
 
 // Every 16-row block position a kernel uses for this read kind and tile.

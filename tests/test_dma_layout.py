@@ -63,9 +63,12 @@ MUTATIONS = [
     ("h_layout.h", "+ (((e >> 3) ^ (xswz(r, row_bytes) << 1)) << 4) + ((e & 7) << 1));",
      "+ (((e >> 3) ^ (xswz(r, row_bytes) << 1)) << 4) + (((e + 1) & 7) << 1));",
      "xtile_off: element off by one within the chunk"),
-    ("h_layout.h", "(((r & 7) << 1) | ((r >> 3) & 1))",
-     "(((r & 7) << 1) | ((r >> 2) & 1))",
+    ("h_layout.h", "((((r & 7) ^ ((r >> 3) & 1)) << 1) | ((r >> 3) & 1))",
+     "((((r & 7) ^ ((r >> 3) & 1)) << 1) | ((r >> 2) & 1))",
      "swz: wrong row bit (bank conflicts)"),
+    ("h_layout.h", "((((r & 7) ^ ((r >> 3) & 1)) << 1) | ((r >> 3) & 1))",
+     "(((r & 7) << 1) | ((r >> 3) & 1))",
+     "swz: bit 3 not folded into the pair index (conflicted score fragments)"),
     ("h_layout.h", "return tile_off(r0 + 4 * (lane >> 4) + ((lane & 15) >> 2), c0 + 4 * (lane & 3), row_bytes);",
      "return tile_off(r0 + 4 * (lane >> 4) + ((lane & 15) >> 2), c0 + 4 * ((lane + 1) & 3), row_bytes);",
      "tr_frag_off: column group of the neighbouring lane"),

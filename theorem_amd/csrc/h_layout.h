@@ -6,15 +6,19 @@
 // A chunk tile is 64 rows (tokens) of `row_bytes` = 128 or 256 bytes (64 / 128
 // bf16 features), stored in LDS without padding.  The 16-byte chunks of row r
 // are XOR-swizzled: logical chunk q sits at physical chunk q ^ swz(r).  The
-// swizzle makes the two read patterns of the kernel conflict-free per 256-byte
-// pass:
+// swizzle makes the three read patterns of the kernels conflict-free:
 //   * 16 consecutive rows (16-aligned), one 16-byte chunk each (w rows as the
-//     A operand, paired order): swz takes 16 distinct values over those rows
-//     (row_bytes 256), or distinct values per row parity (row_bytes 128, two
-//     rows per 256 bytes);
+//     A operand, paired order, two 8-byte reads per 256-byte pass): swz takes
+//     16 distinct values over those rows (row_bytes 256), or distinct values
+//     per row parity (row_bytes 128, two rows per 256 bytes);
 //   * 8 consecutive rows (8-aligned), one aligned 32-byte chunk pair each
 //     (ds_read_b64_tr_b16 fragments of k^T and of the u tile): swz >> 1 takes 8
-//     distinct values (row_bytes 256) or 4 per row parity (row_bytes 128).
+//     distinct values (row_bytes 256) or 4 per row parity (row_bytes 128);
+//   * 16-byte reads of 16 consecutive rows at two adjacent chunks (the fused
+//     kernel's score fragments), which gfx950 serves 32 lanes over 512 bytes
+//     at a time: swz >> 1 takes 8 distinct values within each row parity
+//     (row_bytes 256), or 4 over each class of rows mod 4 (row_bytes 128).
+//     Hence the XOR of bit 3 into the pair index.
 // A DMA instruction writes 1 KiB = 64 lanes x 16 bytes at consecutive physical
 // chunks; lane data is fetched from the logical chunk that belongs there.
 #pragma once
@@ -31,8 +35,8 @@ namespace thm {
 namespace hl {
 
 THM_HD constexpr int swz(int r, int row_bytes) {
-  return row_bytes == 256 ? (((r & 7) << 1) | ((r >> 3) & 1))
-                          : ((((r >> 1) & 3) << 1) | ((r >> 3) & 1));
+  return row_bytes == 256 ? ((((r & 7) ^ ((r >> 3) & 1)) << 1) | ((r >> 3) & 1))
+                          : (((((r >> 1) & 3) ^ ((r >> 3) & 1)) << 1) | ((r >> 3) & 1));
 }
 
 // Byte offset within the tile of bf16 element e of row r.
