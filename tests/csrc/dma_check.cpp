@@ -15,11 +15,13 @@
 //     (64 banks of 4 bytes and 32 lanes per pass for 8-byte reads; 16-byte
 //     reads as measured on gfx950, 32 lanes per pass over 128 banks);
 //   * stores: h, v_new and o tiles are covered exactly once, aligned;
-//   * global bounds: every DMA source, L2 prefetch and store of the extreme
+//   * global bounds: every DMA source and store of the extreme
 //     (batch, head, chunk) lies inside its tensor, and the per-lane offsets fit
 //     in 32 bits; the workgroup -> (b * H + head, V-tile) map is a bijection;
 //   * wait counts: replaying each wave's issue order, the vmcnt the kernel
-//     waits for at the top of chunk c retires exactly the DMA of chunk c;
+//     waits for at the top of chunk c retires exactly the DMA of chunk c (in
+//     the fused kernel, whose w / u DMA runs ahead of its k / q DMA, each
+//     slot is also loaded only after its previous chunk's last read);
 //   * recompute_w_u's [k | v] tile and chunk_fwd_o's v, h and k tiles
 //     (padded, register-staged): the fragments hold the elements the products
 //     need and are read conflict-free; staging stores are bounded in
@@ -378,8 +380,6 @@ static void check_fused() {
     reg.push_back({lp, lp + C::kPBytes});
     reg.push_back({lp + C::kPBytes, lp + C::kPBytes + C::kSBytes});
     reg.push_back({lp + C::kPBytes + C::kSBytes, lp + C::kPBytes + C::kSBytes + C::kVBytes});
-    const int tr = lp + C::kPBytes + C::kSBytes + C::kVBytes;
-    reg.push_back({tr, tr + 256});
     for (size_t i = 0; i < reg.size(); ++i) {
       CHECK(reg[i].first % 16 == 0 && reg[i].second <= C::kLds, "%s: LDS region %zu", what, i);
       for (size_t j = 0; j < i; ++j)
@@ -398,17 +398,6 @@ static void check_fused() {
     const int64_t NT = sh.T / 64, b = sh.B - 1, hh = sh.H - 1, cc = NT - 1;
     const int64_t kc0 = ((b * sh.T) * sh.H + hh) * K * 2;
     const int64_t uc0 = ((b * sh.T) * sh.H + hh) * V * 2 + (V - 64) * 2;
-    // L2 prefetch lines (4-byte DMAs): k / w / q rows for waves 0-2, u rows
-    // (and the gates) for wave 3.
-    for (int i = 0; i < 4; ++i)
-      for (int lane = 0; lane < 64; ++lane) {
-        const uint32_t ok = hl::l2_line_off(i * 64 + lane, C::kRowK, tsk);
-        CHECK((ok % tsk) + 4 <= (uint32_t)C::kRowK && ok / tsk < 64, "%s: k prefetch line outside the rows", what);
-        CHECK(kc0 + cc * 64 * tsk + ok + 4 <= sh.B * sh.T * sh.H * K * 2, "%s: k prefetch past the tensor", what);
-        const uint32_t ou = hl::l2_line_off((i & 1) * 64 + lane, C::kRowU, tsv);
-        CHECK((ou % tsv) + 4 <= (uint32_t)C::kRowU && ou / tsv < 64, "%s: u prefetch line outside the rows", what);
-        CHECK(uc0 + cc * 64 * tsv + ou + 4 <= sh.B * sh.T * sh.H * V * 2, "%s: u prefetch past the tensor", what);
-      }
     // Stores of o and v_new: [64 tokens x V] per chunk, quad-transposed lanes.
     Cover co(64, V);
     for (int vt = 0; vt < V / 64; ++vt)
@@ -418,19 +407,39 @@ static void check_fused() {
                      tsv, 2, what);
     co.exactly_once(what);
   }
-  // Wait counts of the state waves: prologue DMA(0) + prefetch; per chunk the
-  // DMA of c + 1 (4 parts), the prefetch of c + 2, the v_new stores of c.
+  // Slot lifetimes, in phases (2c: phase 1 of chunk c, 2c + 1: phase 2, a
+  // barrier between any two).  Chunk x's k, q and gates are read in phases 2x
+  // and 2x + 1 and DMA'd in phase 2x - 2 (P1 of chunk x - 1); its w and u are
+  // read in phase 2x (P1) only and DMA'd in phase 2x - 3 (after the mid-chunk
+  // barrier of chunk x - 2; the prologue for x <= 1).  Each DMA must come after
+  // the last read of the slot's previous occupant, chunk x - 2, and before the
+  // first read of its own chunk.
+  {
+    const int kq_issue = -2, kq_last_read = 1, wu_issue = -3, wu_last_read = 0;
+    for (int x = 2; x < 6; ++x) {
+      CHECK(2 * x + kq_issue > 2 * (x - 2) + kq_last_read && 2 * x + kq_issue < 2 * x,
+            "%s: k / q DMA of chunk %d overlaps a reader", what, x);
+      CHECK(2 * x + wu_issue > 2 * (x - 2) + wu_last_read && 2 * x + wu_issue < 2 * x,
+            "%s: w / u DMA of chunk %d overlaps a reader", what, x);
+    }
+  }
+  // Wait counts of the state waves.  Prologue: w / u and k / q / g of chunk 0,
+  // w / u of chunk 1.  Chunk c: in P1 the k / q / g DMA of c + 1 and the
+  // v_new stores of c; after the mid-chunk barrier the w / u DMA of c + 2.
+  // Chunk indices past the end are clamped to NT - 1 and loaded again into a
+  // slot no later chunk reads: DMAs of no awaited chunk.
   for (int NT = 1; NT <= 5; ++NT)
     for (int wq = 0; wq < 4; ++wq) {
       WaveOps w;
-      const int nd = 3 * C::kKDma + C::kUDma + ((HAS_G && wq == 0) ? 1 : 0);
-      w.dma(0, nd);
-      w.other(C::kPf);
+      const int nkq = 2 * C::kKDma + ((HAS_G && wq == 0) ? 1 : 0);
+      w.dma(0, C::kWuDma);
+      w.dma(0, nkq);
+      w.dma(NT > 1 ? 1 : -2, C::kWuDma);
       for (int c = 0; c < NT; ++c) {
         w.check_wait(c, c < pipe::kFStages - 1 ? C::kWaitFirst : C::kWaitSteady, what, c);
-        w.dma(c + 1 < NT ? c + 1 : -2, nd);
-        w.other(C::kPf);
+        w.dma(c + 1 < NT ? c + 1 : -2, nkq);
         w.other(C::kStores);
+        w.dma(c + 2 < NT ? c + 2 : -2, C::kWuDma);
       }
     }
 }

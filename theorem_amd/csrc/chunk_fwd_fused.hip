@@ -16,8 +16,10 @@
 // two roles that share SIMDs pairwise; wave role and column group wq (columns
 // 16 wq .. 16 wq + 15 of the tile) are wave-uniform:
 //   * k, w, q, u and g of a chunk arrive by global -> LDS DMA into a 2-stage
-//     ring (XOR-swizzled tiles of h_layout.h), one chunk ahead of use, issued
-//     by the state waves;
+//     ring (XOR-swizzled tiles of h_layout.h), issued by the state waves: k, q
+//     and g in P1 of the chunk before, w and u (read by P1 only) after the
+//     mid-chunk barrier of the chunk two before, into the slots that chunk's
+//     P1 has just finished with;
 //   * state waves (0-3) hold S[K x 16 columns] in fp32 registers.  Phase 1:
 //     hand S to the output waves as bf16 B-operand pairs (LDS), P1 v_new =
 //     u - w S (the S pairs as the B operand, paired contraction order), hand
@@ -33,8 +35,8 @@
 //   * a barrier at the top of each chunk (its tiles are in LDS, chunk c - 1
 //     is finished) and one between the phases.
 // All DMA and stores of the chunk loop go through vmem.h, and the state waves'
-// wait at the top of the loop is an exact count (their v_new stores of one
-// chunk are issued after each chunk's DMA); the output waves issue stores only.
+// wait at the top of the loop is an exact count of the ops they issue after
+// the chunk's k / q DMA (pipe_cfg.h FCfg); the output waves issue stores only.
 // HBM traffic per token-head: k, w and q (K eb each), u (V eb) and g (4 B)
 // read once; o (V eb) written once (+ v_new when requested).  The V-tiles of
 // one (b, head) run on one XCD, so their second read of k, w, q is meant to
@@ -49,7 +51,6 @@ namespace {
 
 using pipe::FCfg;
 using pipe::kBT;
-using pipe::kFPrefetch;
 using pipe::kFStages;
 using pipe::kFThreads;
 constexpr int kFBV = pipe::kTileV;  // V-tile width
@@ -88,7 +89,6 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   // Hand-over slots, lane-major: 16 bytes per lane per B-operand pair.
   bf16x8* const ls = reinterpret_cast<bf16x8*>(lp + C::kPBytes) + wq * KB2 * 64 + lane;
   bf16x8* const lv = reinterpret_cast<bf16x8*>(lp + C::kPBytes + C::kSBytes) + wq * 2 * 64 + lane;
-  char* const ltrash = lp + C::kPBytes + C::kSBytes + C::kVBytes;
 
   // Global geometry in bytes.  Token t of chunk c, head hh: ((b T + 64 c + t) H + hh) D.
   const int64_t tsk = H * K * 2, tsv = H * V * 2;
@@ -110,21 +110,23 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   }
   const uint32_t goff = (uint32_t)(lane * H * 4);
 
-  // Part m of the DMA of chunk cc into stage s: m = 0, 1, 2 the k, w, q tile,
-  // m = 3 the u tile and the gates.
+  // DMA of chunk cc's [64 x K] tile of src (k, w or q) into dst.
+  auto issue_tile = [&](const bf16* src, int64_t cc, char* dst) {
+    const char* sb = reinterpret_cast<const char*>(src) + kc0 + cc * kcs;
+    const uint32_t l0 = lds_address(dst) + wq * C::kKDma * 1024;
+#pragma unroll
+    for (int i = 0; i < C::kKDma; ++i) dma_b128(sb, koff[i], __builtin_amdgcn_readfirstlane(l0 + i * 1024));
+  };
+  // Part m of the DMA of chunk cc's k, q and gates into stage s (P1 of the
+  // chunk before): m = 0 the k tile, 1 the q tile, 2 the gates.  One copy of
+  // the gates (state wave 0): a 64-lane gather at a 4 H-byte stride is the
+  // costliest DMA instruction per byte.
   auto issue_part = [&](int64_t cc, int s, int m) {
-    const int64_t off = kc0 + cc * kcs;
-    if (m < 3) {
-      const char* src = reinterpret_cast<const char*>(m == 0 ? k : m == 1 ? w : q) + off;
-      char* dst = m == 0 ? stage_k(s) : m == 1 ? stage_w(s) : stage_q(s);
-      const uint32_t l0 = lds_address(dst) + wq * C::kKDma * 1024;
-#pragma unroll
-      for (int i = 0; i < C::kKDma; ++i) dma_b128(src, koff[i], __builtin_amdgcn_readfirstlane(l0 + i * 1024));
-    } else {
-      const char* ub = reinterpret_cast<const char*>(u) + uc0 + cc * ucs;
-      const uint32_t lu = lds_address(stage_u(s)) + wq * C::kUDma * 1024;
-#pragma unroll
-      for (int i = 0; i < C::kUDma; ++i) dma_b128(ub, uoff[i], __builtin_amdgcn_readfirstlane(lu + i * 1024));
+    if (m == 0) {
+      issue_tile(k, cc, stage_k(s));
+    } else if (m == 1) {
+      issue_tile(q, cc, stage_q(s));
+    } else if (m == 2) {
       if constexpr (HAS_G) {
         if (wq == 0) {
           const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
@@ -133,75 +135,13 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       }
     }
   };
-  // DMA of chunk cc into stage s; issued by the state waves only.
-  auto issue = [&](int64_t cc, int s) {
-    const int64_t off = kc0 + cc * kcs;
-    const char* srcs[3] = {reinterpret_cast<const char*>(k) + off, reinterpret_cast<const char*>(w) + off,
-                           reinterpret_cast<const char*>(q) + off};
-    char* dsts[3] = {stage_k(s), stage_w(s), stage_q(s)};
-#pragma unroll
-    for (int m = 0; m < 3; ++m) {
-      const uint32_t l0 = lds_address(dsts[m]) + wq * C::kKDma * 1024;
-#pragma unroll
-      for (int i = 0; i < C::kKDma; ++i) dma_b128(srcs[m], koff[i], __builtin_amdgcn_readfirstlane(l0 + i * 1024));
-    }
+  // DMA of chunk cc's w and u tiles into stage s.
+  auto issue_wu = [&](int64_t cc, int s) {
+    issue_tile(w, cc, stage_w(s));
     const char* ub = reinterpret_cast<const char*>(u) + uc0 + cc * ucs;
     const uint32_t lu = lds_address(stage_u(s)) + wq * C::kUDma * 1024;
 #pragma unroll
     for (int i = 0; i < C::kUDma; ++i) dma_b128(ub, uoff[i], __builtin_amdgcn_readfirstlane(lu + i * 1024));
-    if constexpr (HAS_G) {
-      // One copy of the gates (state wave 0): a 64-lane gather at a 4 H-byte
-      // stride is the costliest DMA instruction per byte.
-      if (wq == 0) {
-        const char* gb = reinterpret_cast<const char*>(g) + gc0 + cc * gcs;
-        dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s))));
-      }
-    }
-  };
-
-  // L2 prefetch of chunk cc (state waves): one 4-byte DMA per 64-byte line of
-  // the chunk's tiles, landing in a scratch LDS slot whose contents are never
-  // read, so the DMA of that chunk one iteration later finds its lines in L2.
-  // Waves 0, 1, 2 cover the k, w, q rows (up to 256 lines each), wave 3 the
-  // u rows of the V-tile and the gates; surplus lanes repeat lines.
-  uint32_t pfo[4];
-  {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (wq < 3) {
-        pfo[i] = hl::l2_line_off(i * 64 + lane, C::kRowK, tsk);
-      } else {
-        pfo[i] = (HAS_G && i >= 2) ? goff : hl::l2_line_off((i & 1) * 64 + lane, C::kRowU, tsv);
-      }
-    }
-  }
-  // Per-wave prefetch sources (instructions 0-1 from pfa, 2-3 from pfb), chunk strides.
-  const char* pfa;
-  const char* pfb;
-  int64_t pfsa, pfsb;
-  if (wq < 3) {
-    pfa = (wq == 0 ? reinterpret_cast<const char*>(k) : wq == 1 ? reinterpret_cast<const char*>(w)
-                                                                : reinterpret_cast<const char*>(q)) + kc0;
-    pfb = pfa;
-    pfsa = pfsb = kcs;
-  } else {
-    pfa = reinterpret_cast<const char*>(u) + uc0;
-    pfsa = ucs;
-    pfb = HAS_G ? reinterpret_cast<const char*>(g) + gc0 : pfa;
-    pfsb = HAS_G ? gcs : ucs;
-  }
-  pfa = reinterpret_cast<const char*>(uniform_ptr(pfa));
-  pfb = reinterpret_cast<const char*>(uniform_ptr(pfb));
-  auto prefetch = [&](int64_t cc) {
-    if constexpr (kFPrefetch) {
-      const uint32_t lt = __builtin_amdgcn_readfirstlane(lds_address(ltrash));
-      const char* a = pfa + cc * pfsa;
-      const char* bb = pfb + cc * pfsb;
-      dma_b32(a, pfo[0], lt);
-      dma_b32(a, pfo[1], lt);
-      dma_b32(bb, pfo[2], lt);
-      dma_b32(bb, pfo[3], lt);
-    }
   };
 
   // rows x S for a 16-row block of a [64 x K] tile (w or q): A = tile rows,
@@ -242,8 +182,10 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   wait_vmcnt<0>();  // retire the h0 loads before the counted loop
 
   if (state_wave && NT > 0) {
-    issue(0, 0);
-    prefetch(NT > 1 ? 1 : 0);
+    issue_wu(0, 0);
+#pragma unroll
+    for (int m = 0; m < 3; ++m) issue_part(0, 0, m);
+    issue_wu(NT > 1 ? 1 : 0, 1);
   }
   for (int64_t c = 0; c < NT; ++c) {
     const int s = (int)(c % kFStages);
@@ -272,8 +214,8 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       }
     }
     if (state_wave) {
-      // The next chunk's DMA is issued in four parts between P1's row blocks,
-      // so the address unit drains between parts while the MFMAs run.
+      // The next chunk's k / q / g DMA is issued in parts between P1's row
+      // blocks, so the address unit drains between parts while the MFMAs run.
       const int64_t cn = c + kFStages - 1;
       const int64_t cnc = cn < NT ? cn : NT - 1;
       const int cns = (int)(cn % kFStages);
@@ -297,7 +239,6 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
         for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
         vn[jb] -= rows_times_S(tw, jb, sb);
       }
-      prefetch(cn + 1 < NT ? cn + 1 : NT - 1);
       if constexpr (STORE_VN) {
         bf16* vb = vnew + ((b * T + c * kBT) * H + hh) * V;
 #pragma unroll
@@ -362,6 +303,9 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     lds_barrier();  // M: P, the S pairs and the v_new pairs of chunk c are in LDS
 
     if (state_wave) {
+      // P1 of this chunk is done with stage s's w and u: chunk c + 2's go there
+      // (clamped re-loads at the end land in slots no later chunk reads).
+      issue_wu(c + 2 < NT ? c + 2 : NT - 1, s);
       // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
       bf16x8 vh[2];
       float decay = 1.f;

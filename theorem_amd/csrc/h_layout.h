@@ -77,12 +77,6 @@ THM_HD constexpr uint32_t row8_frag_off(int r0, int e0, int lane, int row_bytes)
   return tile_off(r0 + (lane & 15), e0 + 8 * (lane >> 4), row_bytes);
 }
 
-// L2 prefetch of a chunk's token block: line L (64 bytes) of row
-// (L / lines) % 64, lines = row_bytes / 64; indices past the block wrap.
-THM_HD constexpr uint32_t l2_line_off(int L, int row_bytes, int64_t tok_stride) {
-  return (uint32_t)(((L / (row_bytes / 64)) % 64) * tok_stride + (L % (row_bytes / 64)) * 64);
-}
-
 // Global stores of a 16 x 16 accumulator tile at (r0, c0) of a row-major array
 // (rows `row_stride` bytes apart, `eb` bytes per element), 4 elements per lane.
 // Row-quad layout (after vmem.h acc_to_row_quads): lane (grp, 4 a + b) holds

@@ -57,12 +57,15 @@ struct PCfg {
 
 // ---------------------------------------------------------------------------
 // Fused h + o kernel: 8 wavefronts, state waves 0-3 and output waves 4-7, wave
-// wq = w % 4 on columns 16 wq .. + 15 of the V-tile.  The state waves issue the
-// DMA of chunk c + 1 (k, w, q, u and the gates, in four parts), an L2
-// prefetch of chunk c + 2 and their v_new stores of chunk c.
+// wq = w % 4 on columns 16 wq .. + 15 of the V-tile.  In chunk c the state
+// waves issue the DMA of chunk c + 1's k, q and gates (in parts between P1's
+// row blocks), their v_new stores of chunk c and, after the mid-chunk barrier,
+// the DMA of chunk c + 2's w and u: only P1 reads w and u, so their slots in
+// stage c % 2 are free from that barrier on, and those tiles get one and a half
+// chunk periods to arrive.  There is no L2 prefetch: beside the early w / u
+// DMA, every prefetch variant measured slower.
 constexpr int kFThreads = 512;     // 4 state + 4 output wavefronts
 constexpr int kFStages = 2;
-constexpr bool kFPrefetch = true;  // L2 prefetch of the chunk after the one in flight
 
 template <int K, bool HAS_G, bool STORE_VN>
 struct FCfg {
@@ -76,17 +79,16 @@ struct FCfg {
   static constexpr int kPBytes = kBT * kBT * 2;   // the chunk's scores P, bf16
   static constexpr int kSBytes = 4 * (KB / 2) * 64 * 16;  // S handed over as bf16 B-operand pairs
   static constexpr int kVBytes = 4 * 2 * 64 * 16;         // v_new handed over the same way
-  static constexpr int kTrash = 256;                      // landing slot of the L2 prefetch DMAs
-  static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes + kTrash;
+  static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes;
   static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per state wave per k / w / q tile
   static constexpr int kUDma = kTileU / 1024 / 4;
-  static constexpr int kDma = 3 * kKDma + kUDma + (HAS_G ? 1 : 0);
+  static constexpr int kWuDma = kKDma + kUDma;    // a chunk's w and u tiles, per state wave
   static constexpr int kStores = STORE_VN ? 4 : 0;  // v_new row tiles per state wave
-  static constexpr int kPf = kFPrefetch ? 4 : 0;    // L2 prefetch DMAs per state wave per chunk
-  // Ops a state wave issues after the DMA of chunk c before it waits for it:
-  // the prefetch of chunk c + 1 (and, from c = 1 on, the stores of chunk c - 1).
-  static constexpr int kWaitFirst = kPf;
-  static constexpr int kWaitSteady = kPf + kStores;
+  // Ops a state wave issues after the k / q DMA of chunk c before it waits for
+  // it: from c = 1 on the v_new stores of chunk c - 1, then the w / u DMA of
+  // chunk c + 1.  The w / u DMA of chunk c was issued before that k / q DMA.
+  static constexpr int kWaitFirst = kWuDma;
+  static constexpr int kWaitSteady = kStores + kWuDma;
   static_assert(kFStages == 2, "the wait counts assume double buffering");
   static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
   static_assert(kLds <= 160 * 1024, "LDS budget");
