@@ -175,6 +175,36 @@ def test_fused_forward_matches_two_kernels_and_oracle(dev, K, V, gate):
     assert torch.equal(ht0, d["h0"])
 
 
+@pytest.mark.parametrize("K,V", [(64, 64), (128, 128)])
+@pytest.mark.parametrize("T", [64, 128, 192])
+def test_fused_forward_short_sequences(dev, K, V, T):
+    # One to three chunks: the fused kernel's prologue loads chunk 0 and the
+    # w / u of chunk 1, and each chunk loads the w / u of the chunk two ahead,
+    # so here the prologue and the end-of-sequence re-loads (chunk indices
+    # clamped to the last chunk) overlap.  Carry-visible gate and h0, against
+    # the two kernels and the float64 oracle.
+    from theorem_amd.kernels import chunk_fwd_h, chunk_fwd_o
+    B, H = 2, 3
+    d = configs.make_h_inputs(B, T, H, K, V, seed=33, device=dev, dtype=torch.bfloat16, gate="mild", h0_std=0.1)
+    gen = torch.Generator().manual_seed(34)
+    q = configs.l2norm(torch.randn(B, T, H, K, generator=gen)).to(torch.bfloat16).to(dev)
+    scale = K ** -0.5
+    o, vn, ht = chain.chunk_fwd_fused(q, d["k"], d["w"], d["u"], d["g"], scale, d["h0"], True, True)
+    h, vn2, ht2 = chunk_fwd_h.custom_kernel(dict(k=d["k"], w=d["w"], u=d["u"], g=d["g"], initial_state=d["h0"],
+                                                 output_final_state=True))
+    o2 = chunk_fwd_o.custom_kernel(dict(q=q, k=d["k"], v=vn2, g=d["g"], h=h, scale=scale))
+    torch.cuda.synchronize()
+    assert_close(o, o2, 1e-2, 1e-2, f"fused o vs two kernels K={K} T={T}")
+    assert_close(vn, vn2, 1e-2, 1e-2, "v_new")
+    assert_close(ht, ht2, 1e-2, 1e-2, "final state")
+    gk = np_(d["g"])
+    eh, evn, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np_(d["w"]), np_(d["u"]), gk, h0=np_(d["h0"]))
+    eo = odn.chunk_fwd_o_diff(np_(q), np_(d["k"]), evn, gk, eh, scale)
+    assert_close(o, eo, 1e-2, 1e-2, f"fused o vs oracle K={K} T={T}")
+    assert_close(vn, evn, 1e-2, 1e-2, "v_new vs oracle")
+    assert_close(ht, eht, 1e-2, 1e-2, "final state vs oracle")
+
+
 @pytest.mark.parametrize("K,V", [(64, 64), (64, 128), (128, 64), (128, 128)])
 @pytest.mark.parametrize("sign", [1, -1])
 @pytest.mark.parametrize("gate", ["logsigmoid", None])
