@@ -407,39 +407,36 @@ static void check_fused() {
                      tsv, 2, what);
     co.exactly_once(what);
   }
-  // Slot lifetimes, in phases (2c: phase 1 of chunk c, 2c + 1: phase 2, a
-  // barrier between any two).  Chunk x's k, q and gates are read in phases 2x
-  // and 2x + 1 and DMA'd in phase 2x - 2 (P1 of chunk x - 1); its w and u are
-  // read in phase 2x (P1) only and DMA'd in phase 2x - 3 (after the mid-chunk
-  // barrier of chunk x - 2; the prologue for x <= 1).  Each DMA must come after
-  // the last read of the slot's previous occupant, chunk x - 2, and before the
-  // first read of its own chunk.
-  {
-    const int kq_issue = -2, kq_last_read = 1, wu_issue = -3, wu_last_read = 0;
-    for (int x = 2; x < 6; ++x) {
-      CHECK(2 * x + kq_issue > 2 * (x - 2) + kq_last_read && 2 * x + kq_issue < 2 * x,
-            "%s: k / q DMA of chunk %d overlaps a reader", what, x);
-      CHECK(2 * x + wu_issue > 2 * (x - 2) + wu_last_read && 2 * x + wu_issue < 2 * x,
-            "%s: w / u DMA of chunk %d overlaps a reader", what, x);
-    }
+  // Slot lifetimes of the issue schedule (FCfg kKqLead, kWuLead), in phases
+  // (2c: phase 1 of chunk c, 2c + 1: phase 2, a barrier between any two).
+  // Chunk x's k, q and gates are read in phases 2x and 2x + 1 and DMA'd in
+  // phase 2(x - kKqLead) (P1); its w and u are read in phase 2x (P1) only
+  // and DMA'd in phase 2(x - kWuLead) + 1, after the mid-chunk barrier.  Each
+  // lands in stage x % 2, whose previous occupant is chunk x - 2: the DMA
+  // must come after that chunk's last read and before its own chunk's first.
+  for (int x = 2; x < 6; ++x) {
+    const int kq_issue = 2 * (x - C::kKqLead), wu_issue = 2 * (x - C::kWuLead) + 1;
+    CHECK(kq_issue > 2 * (x - 2) + 1 && kq_issue < 2 * x, "%s: k / q DMA of chunk %d overlaps a reader", what, x);
+    CHECK(wu_issue > 2 * (x - 2) && wu_issue < 2 * x, "%s: w / u DMA of chunk %d overlaps a reader", what, x);
   }
-  // Wait counts of the state waves.  Prologue: w / u and k / q / g of chunk 0,
-  // w / u of chunk 1.  Chunk c: in P1 the k / q / g DMA of c + 1 and the
-  // v_new stores of c; after the mid-chunk barrier the w / u DMA of c + 2.
-  // Chunk indices past the end are clamped to NT - 1 and loaded again into a
-  // slot no later chunk reads: DMAs of no awaited chunk.
+  // Wait counts of the state waves, replaying the kernel's issue order.
+  // Prologue: w / u and k / q / g of chunk 0, then w / u of chunks 1 ..
+  // kWuLead - 1.  Chunk c: in P1 the k / q / g DMA of c + kKqLead and the
+  // v_new stores of c; after the mid-chunk barrier the w / u DMA of
+  // c + kWuLead.  Chunk indices past the end are clamped to NT - 1 and loaded
+  // again into a slot no later chunk reads: DMAs of no awaited chunk.
   for (int NT = 1; NT <= 5; ++NT)
     for (int wq = 0; wq < 4; ++wq) {
       WaveOps w;
       const int nkq = 2 * C::kKDma + ((HAS_G && wq == 0) ? 1 : 0);
       w.dma(0, C::kWuDma);
       w.dma(0, nkq);
-      w.dma(NT > 1 ? 1 : -2, C::kWuDma);
+      for (int x = 1; x < C::kWuLead; ++x) w.dma(x < NT ? x : -2, C::kWuDma);
       for (int c = 0; c < NT; ++c) {
         w.check_wait(c, c < pipe::kFStages - 1 ? C::kWaitFirst : C::kWaitSteady, what, c);
-        w.dma(c + 1 < NT ? c + 1 : -2, nkq);
+        w.dma(c + C::kKqLead < NT ? c + C::kKqLead : -2, nkq);
         w.other(C::kStores);
-        w.dma(c + 2 < NT ? c + 2 : -2, C::kWuDma);
+        w.dma(c + C::kWuLead < NT ? c + C::kWuLead : -2, C::kWuDma);
       }
     }
 }

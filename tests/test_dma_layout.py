@@ -99,12 +99,16 @@ MUTATIONS = [
     ("pipe_cfg.h", "static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma;",
      "static constexpr int kWaitSteady = (NS - 1) * kStores + (NS - 2) * kDma + 1;",
      "chunk_fwd_h: steady-state wait one op too loose"),
-    ("pipe_cfg.h", "static constexpr int kWaitSteady = kStores + kWuDma;",
-     "static constexpr int kWaitSteady = kStores + kWuDma - 1;",
+    ("pipe_cfg.h", "static constexpr int kWaitSteady = kWuLead >= 2 ? kStores + kWuDma : 0;",
+     "static constexpr int kWaitSteady = kWuLead >= 2 ? kStores + kWuDma - 1 : 0;",
      "fused: steady-state wait one op too tight"),
-    ("pipe_cfg.h", "static constexpr int kWaitFirst = kWuDma;",
-     "static constexpr int kWaitFirst = kWuDma + 1;",
-     "fused: first wait ignores the early w / u DMA order (one op too loose)"),
+    ("pipe_cfg.h", "static constexpr int kWaitFirst = (kWuLead - 1) * kWuDma;",
+     "static constexpr int kWaitFirst = (kWuLead - 1) * kWuDma + 1;",
+     "fused: first wait one op too loose"),
+    ("pipe_cfg.h", "  static constexpr int kWuLead = 2;", "  static constexpr int kWuLead = 3;",
+     "fused: w / u DMA three chunks ahead (overwrites a slot still in use)"),
+    ("pipe_cfg.h", "  static constexpr int kKqLead = 1;", "  static constexpr int kKqLead = 2;",
+     "fused: k / q DMA two chunks ahead (overwrites a slot still in use)"),
     ("h_layout.h", "THM_HD constexpr int spiece_row(int m, int it, int n, int ml) { return m / (n / 8) + it * (ml / (n / 8)); }",
      "THM_HD constexpr int spiece_row(int m, int it, int n, int ml) { return m / (n / 8) + it * (ml / (n / 4)); }",
      "small chunk_fwd_h: load pieces at the wrong row stride"),

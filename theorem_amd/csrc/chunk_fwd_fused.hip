@@ -185,7 +185,8 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     issue_wu(0, 0);
 #pragma unroll
     for (int m = 0; m < 3; ++m) issue_part(0, 0, m);
-    issue_wu(NT > 1 ? 1 : 0, 1);
+#pragma unroll
+    for (int x = 1; x < C::kWuLead; ++x) issue_wu(x < NT ? x : NT - 1, x % kFStages);
   }
   for (int64_t c = 0; c < NT; ++c) {
     const int s = (int)(c % kFStages);
@@ -216,7 +217,7 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     if (state_wave) {
       // The next chunk's k / q / g DMA is issued in parts between P1's row
       // blocks, so the address unit drains between parts while the MFMAs run.
-      const int64_t cn = c + kFStages - 1;
+      const int64_t cn = c + C::kKqLead;
       const int64_t cnc = cn < NT ? cn : NT - 1;
       const int cns = (int)(cn % kFStages);
       // S as the B operand (pairs of 16-row tiles), also handed to the output wave.
@@ -303,9 +304,11 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     lds_barrier();  // M: P, the S pairs and the v_new pairs of chunk c are in LDS
 
     if (state_wave) {
-      // P1 of this chunk is done with stage s's w and u: chunk c + 2's go there
-      // (clamped re-loads at the end land in slots no later chunk reads).
-      issue_wu(c + 2 < NT ? c + 2 : NT - 1, s);
+      // P1 of this chunk is done with its w and u: chunk c + kWuLead's go to
+      // that chunk's stage (clamped re-loads at the end land in slots no later
+      // chunk reads).
+      const int64_t cw = c + C::kWuLead;
+      issue_wu(cw < NT ? cw : NT - 1, (int)(cw % kFStages));
       // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}).
       bf16x8 vh[2];
       float decay = 1.f;

@@ -84,11 +84,17 @@ struct FCfg {
   static constexpr int kUDma = kTileU / 1024 / 4;
   static constexpr int kWuDma = kKDma + kUDma;    // a chunk's w and u tiles, per state wave
   static constexpr int kStores = STORE_VN ? 4 : 0;  // v_new row tiles per state wave
+  // Issue schedule, in chunks of lead: chunk x's k, q and gates are DMA'd in
+  // P1 of chunk x - kKqLead, its w and u after the mid-chunk barrier of chunk
+  // x - kWuLead (chunks x < kWuLead in the prologue), each into stage x % 2.
+  static constexpr int kKqLead = 1;
+  static constexpr int kWuLead = 2;
   // Ops a state wave issues after the k / q DMA of chunk c before it waits for
   // it: from c = 1 on the v_new stores of chunk c - 1, then the w / u DMA of
-  // chunk c + 1.  The w / u DMA of chunk c was issued before that k / q DMA.
-  static constexpr int kWaitFirst = kWuDma;
-  static constexpr int kWaitSteady = kStores + kWuDma;
+  // chunk c - 1 + kWuLead (chunk c's own when kWuLead = 1: nothing after it).
+  // At c = 0, the prologue's w / u DMA of chunks 1 .. kWuLead - 1.
+  static constexpr int kWaitFirst = (kWuLead - 1) * kWuDma;
+  static constexpr int kWaitSteady = kWuLead >= 2 ? kStores + kWuDma : 0;
   static_assert(kFStages == 2, "the wait counts assume double buffering");
   static_assert(kStage % 1024 == 0, "1 KiB aligned stages");
   static_assert(kLds <= 160 * 1024, "LDS budget");
