@@ -28,8 +28,10 @@
 //     conflicts;
 //   * the fused WY kernel's [k | v] tile (nat_row order): staging, transposed
 //     reads and form_L's row reads, all conflict-free;
-//   * chunk_fwd_o's pipelined kernel: its walk (desc_walk_*) visits every tile
-//     once, in descending chunk order, and its load offsets (o_*_lane /
+//   * chunk_fwd_o's pipelined kernel: its walk (desc_walk_at) maps walk
+//     indices to tiles one to one, in descending chunk order; its run-time
+//     hand-out of walk indices (dyn_tile) processes each exactly once; and its
+//     load offsets (o_*_lane /
 //     o_*_step) read exactly the elements its staging writes, in bounds and
 //     in 32 bits up to the entry point's limit on H.
 // Exit status 0 and "dma_check: ok" on success; the first failures are printed.
@@ -774,24 +776,64 @@ static void check_o_walk() {
                         {1, 260, 2, 512},  {2, 3, 5, 7},     {5, 1, 3, 2},     {8, 16, 128, 1024}, {7, 9, 11, 100}};
   for (const Case& c : cases) {
     const uint32_t tiles = c.B * c.NT * c.H;
+    // Walk index -> tile: a bijection, head fastest, chunks in descending order.
     std::vector<int> seen(tiles, 0);
-    const hl::DescWalk step = hl::desc_walk_at(c.G, c.B, c.H);
-    CHECK(step.b < c.B && step.hh < c.H, "o walk step (%u, %u, %u)", step.cq, step.b, step.hh);
-    for (uint32_t wg = 0; wg < std::min(c.G, tiles); ++wg) {
-      hl::DescWalk w = hl::desc_walk_at(wg, c.B, c.H);
-      for (uint32_t t = wg; t < tiles; t += c.G) {
-        const uint32_t bh = c.B * c.H, cq = t / bh, b = (t % bh) / c.H, hh = t % c.H;
-        CHECK(w.cq == cq && w.b == b && w.hh == hh, "o walk B=%u H=%u G=%u: t=%u at (%u,%u,%u), want (%u,%u,%u)", c.B,
-              c.H, c.G, t, w.cq, w.b, w.hh, cq, b, hh);
-        if (w.cq >= c.NT || w.b >= c.B || w.hh >= c.H) break;
-        const uint32_t tile = (w.b * c.NT + (c.NT - 1 - w.cq)) * c.H + w.hh;
-        ++seen[tile];
-        if (t + c.G < tiles) hl::desc_walk_step(w, step, c.B, c.H);
-      }
+    for (uint32_t t = 0; t < tiles; ++t) {
+      const hl::DescWalk w = hl::desc_walk_at(t, c.B, c.H);
+      const uint32_t bh = c.B * c.H, cq = t / bh, b = (t % bh) / c.H, hh = t % c.H;
+      CHECK(w.cq == cq && w.b == b && w.hh == hh, "o walk B=%u H=%u: t=%u at (%u,%u,%u), want (%u,%u,%u)", c.B, c.H,
+            t, w.cq, w.b, w.hh, cq, b, hh);
+      if (w.cq >= c.NT || w.b >= c.B || w.hh >= c.H) continue;
+      ++seen[(w.b * c.NT + (c.NT - 1 - w.cq)) * c.H + w.hh];
     }
     for (uint32_t tile = 0; tile < tiles; ++tile)
-      CHECK(seen[tile] == 1, "o walk B=%u H=%u NT=%u G=%u: tile %u visited %d times", c.B, c.H, c.NT, c.G, tile,
-            seen[tile]);
+      CHECK(seen[tile] == 1, "o walk B=%u H=%u NT=%u: tile %u at %d walk indices", c.B, c.H, c.NT, tile, seen[tile]);
+    // The run-time hand-out, replayed with the workgroups drawing tickets in
+    // several interleavings: workgroup w takes w (if w < tiles), draws the
+    // tickets of the next two tiles, then per tile processed one more; it
+    // stops at the first tile index past the end.  Every walk index must be
+    // processed exactly once, every workgroup must stop, and a draw it drops
+    // must be past the end.
+    for (uint32_t seed = 1; seed <= 3; ++seed) {
+      struct Wg {
+        uint32_t t, tn, pend;
+        bool live;
+      };
+      std::vector<Wg> wg(c.G);
+      std::vector<int> done(tiles, 0);
+      uint32_t counter = 0, lcg = seed * 2654435761u;
+      auto draw = [&]() { return hl::dyn_tile(c.G, counter++); };
+      for (uint32_t w = 0; w < c.G; ++w) {
+        wg[w].live = w < tiles;
+        if (!wg[w].live) continue;
+        wg[w].t = w;
+        wg[w].tn = draw();
+        wg[w].pend = draw();
+      }
+      for (long steps = 0;; ++steps) {
+        std::vector<uint32_t> live;
+        for (uint32_t w = 0; w < c.G; ++w)
+          if (wg[w].live) live.push_back(w);
+        if (live.empty()) break;
+        CHECK(steps < 4L * (tiles + c.G) + 16, "o hand-out B=%u H=%u NT=%u G=%u: does not stop", c.B, c.H, c.NT, c.G);
+        if (steps >= 4L * (tiles + c.G) + 16) break;
+        lcg = lcg * 1664525u + 1013904223u;
+        Wg& x = wg[live[(lcg >> 8) % live.size()]];
+        CHECK(x.t < tiles, "o hand-out: tile %u past the end processed", x.t);
+        if (x.t < tiles) ++done[x.t];
+        if (x.tn >= tiles) {
+          CHECK(x.pend >= tiles, "o hand-out: a dropped draw %u is a tile", x.pend);
+          x.live = false;
+          continue;
+        }
+        x.t = x.tn;
+        x.tn = x.pend;
+        x.pend = draw();
+      }
+      for (uint32_t t = 0; t < tiles; ++t)
+        CHECK(done[t] == 1, "o hand-out B=%u H=%u NT=%u G=%u seed %u: walk index %u processed %d times", c.B, c.H,
+              c.NT, c.G, seed, t, done[t]);
+    }
   }
 }
 

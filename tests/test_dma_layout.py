@@ -5,7 +5,7 @@ global -> LDS with hand-built 32-bit lane offsets, read them back through an
 XOR swizzle and wait for them with hand-counted vmcnt values; the small-grid
 chunk_fwd_h kernel stages its tiles and hands h and v_new between its waves
 through LDS buffers whose layout it shares with the checker; chunk_fwd_o's
-pipelined kernel walks its tiles with carried coordinates and loads them with
+pipelined kernel hands out its tiles at run time (dyn_tile) and loads them with
 32-bit per-lane offsets.  A slip there
 would fault the GPU or race rather than fail a numerical test, so
 tests/csrc/dma_check.cpp evaluates the very index functions and layout
@@ -127,10 +127,15 @@ MUTATIONS = [
     ("h_layout.h", "  return (sq * 8u + (t & 7u)) * h + (slot - sq * h);",
      "  return (sq * 8u + (t & 7u)) * h + (slot - sq * h) / 2;",
      "xcd_tile_order: head index halved (not a bijection)"),
-    ("h_layout.h", "  if (w.b >= B) {", "  if (w.b > B) {",
-     "chunk_fwd_o walk: batch carry one late"),
-    ("h_layout.h", "  w.cq += step.cq;\n", "",
-     "chunk_fwd_o walk: whole-sweep part of the step dropped"),
+    ("h_layout.h", "const uint32_t bh = B * H, cq = t / bh, r = t - cq * bh, b = r / H;",
+     "const uint32_t bh = B * H, cq = t / bh, r = t - cq * bh, b = r / (H + 1);",
+     "chunk_fwd_o walk: batch index from the wrong divisor"),
+    ("h_layout.h", "THM_HD constexpr uint32_t dyn_tile(uint32_t grid, uint32_t ticket) { return grid + ticket; }",
+     "THM_HD constexpr uint32_t dyn_tile(uint32_t grid, uint32_t ticket) { return grid + ticket - 1; }",
+     "chunk_fwd_o hand-out: first ticket repeats the last workgroup's own tile"),
+    ("h_layout.h", "THM_HD constexpr uint32_t dyn_tile(uint32_t grid, uint32_t ticket) { return grid + ticket; }",
+     "THM_HD constexpr uint32_t dyn_tile(uint32_t grid, uint32_t ticket) { return grid + ticket + 1; }",
+     "chunk_fwd_o hand-out: a tile skipped"),
     ("h_layout.h", "(uint32_t)(tid % (n / 8)) * 8u) * 2u;", "(uint32_t)(tid % (n / 8)) * 4u) * 2u;",
      "chunk_fwd_o: v / k lane offset at half the element stride"),
     ("h_layout.h", "return (int64_t)it * (256 / (V / 4)) * V * 4; }", "return (int64_t)it * (256 / (V / 4)) * V * 2; }",

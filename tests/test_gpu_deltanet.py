@@ -118,6 +118,40 @@ def test_o_pipelined_path(dev, K, V, gate):
     assert_close(o, e, 1e-2, 1e-2, f"o K={K} V={V} gate={gate}")
 
 
+def test_o_pipelined_handout_across_launches_and_streams(dev):
+    # The pipelined kernel hands out its tiles at run time from a counter slot
+    # that the launch's last workgroup resets; the slots rotate per launch.
+    # 300 launches in a row (more than the 256 slots, so every slot is reused
+    # after its reset) and launches alternating between two streams with no
+    # synchronisation between them must all give the first launch's output bit
+    # for bit, and that output must match the oracle.
+    K = V = 64
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    B, H = 1, 16
+    T = 64 * max(2, -(-4 * cus // H))  # at least 2 tiles per persistent workgroup
+    d = configs.make_o_inputs(B, T, H, K, V, seed=21, device=dev, dtype=torch.bfloat16)
+    args = dict(q=d["q"], k=d["k"], v=d["v"], g=d["g"], h=d["h"], scale=d["scale"])
+    o0 = chunk_fwd_o.custom_kernel(args)
+    sync()
+    e = odn.chunk_fwd_o_diff(np_(d["q"]), np_(d["k"]), np_(d["v"]), np_(d["g"]), np_(d["h"]), d["scale"])
+    assert_close(o0, e, 1e-2, 1e-2, "o pipelined")
+    outs = [chunk_fwd_o.custom_kernel(args) for _ in range(300)]
+    sync()
+    bad = [i for i, o in enumerate(outs) if not torch.equal(o, o0)]
+    assert not bad, f"launches {bad[:8]} differ from the first"
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    cur = torch.cuda.current_stream()
+    for s in streams:
+        s.wait_stream(cur)
+    outs = []
+    for i in range(16):
+        with torch.cuda.stream(streams[i % 2]):
+            outs.append(chunk_fwd_o.custom_kernel(args))
+    sync()
+    bad = [i for i, o in enumerate(outs) if not torch.equal(o, o0)]
+    assert not bad, f"two-stream launches {bad} differ from the first"
+
+
 def test_o_closed_forms(dev):
     d = configs.make_o_inputs(1, 128, 2, 64, 64, seed=4, device=dev, dtype=torch.float32)
     q, k, v, h = d["q"], d["k"], d["v"], d["h"]

@@ -24,6 +24,7 @@
 //   3. acc[n][i] += sum_j v[j][n] P[i][j]: the P accumulator pairs are the B
 //      operand in paired order, v^T comes from LDS in the same order;
 //   4. o[i][n..n+3] = scale * acc.
+#include <atomic>
 #include <type_traits>
 
 #include "h_layout.h"
@@ -194,14 +195,30 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
 // With one tile per workgroup the loads of a tile are all in flight before
 // its compute, but nothing loads while it computes; at 3 resident workgroups
 // per CU that leaves HBM idle for a large part of each tile (the kernel with
-// its MFMA work removed runs in 60 % of the time).  Here each workgroup walks
-// tiles t, t + G, t + 2G, ... of a sequence (G = 2 workgroups per CU; the
-// sequence takes the chunks in descending order) and issues the next
-// tile's global loads into registers before computing the current tile from
-// LDS, then stages them to LDS behind a barrier.  k is staged in LDS as well
-// (its fragments are plain 16-byte row reads), which keeps the prefetched set
-// to 28 16-byte loads per thread.  The arithmetic is the kernel above's.
+// its MFMA work removed runs in 60 % of the time).  Here G = 2 workgroups per
+// CU stay resident and take the tiles of a sequence (chunks in descending
+// order) one after another: each issues the next tile's global loads into
+// registers before computing the current tile from LDS, then stages them to
+// LDS behind a barrier.  k is staged in LDS as well (its fragments are plain
+// 16-byte row reads), which keeps the prefetched set to 28 16-byte loads per
+// thread.  The arithmetic is the kernel above's.
+//
+// The tiles are handed out at run time (h_layout.h dyn_tile): each workgroup
+// draws a ticket from a counter for the tile after next, one tile ahead of
+// need, so the atomic's latency stays hidden.  Workgroups on the XCDs that
+// run slower (XCDs 1 and 5 on every box measured) so take fewer tiles; the
+// fixed walk t, t + G, ... waited for them (419.4-419.9 against 400.1 us at
+// config 4, interleaved, o bit-identical).  The counters live in a static
+// device array of kOTileSlots slots, one per launch in rotation; the last
+// workgroup of a launch to finish resets its slot for the next use.  So up
+// to kOTileSlots launches may be in flight on one device at once (across
+// streams) before two of them could share a counter.
 constexpr int kOPipeWGsPerCU = 2;
+constexpr int kOTileSlots = 256;
+
+// Slot s: {next ticket, workgroups finished}.  Device code uses it by name;
+// host code never passes its address (it passes the slot index).
+__device__ __align__(256) unsigned int g_o_tiles[kOTileSlots][2];
 
 template <int K, int V>
 struct OPCfg {
@@ -223,7 +240,7 @@ __global__ void __launch_bounds__(kOThreads, 2)
 chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                         const bf16* __restrict__ v, const float* __restrict__ g,
                         const float* __restrict__ hs, bf16* __restrict__ o, float scale, int64_t T,
-                        int64_t H, int64_t NT, int64_t tiles) {
+                        int64_t H, int64_t NT, int64_t tiles, uint32_t slot) {
   using C = OPCfg<K, V>;
   constexpr int KS = C::KS;
   constexpr int NB = V / 16;
@@ -239,16 +256,16 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   const int li = lane & 15;
   const int i = 16 * wv + li;  // this lane's query position
 
-  // Walk order (h_layout.h desc_walk_*): head fastest, chunks in descending
+  // Walk order (h_layout.h desc_walk_at): head fastest, chunks in descending
   // order.  This kernel takes the same time in either order, but the kernel
   // that runs after it does not: the next step's recompute_w_u (after the
   // conv or directly after this kernel, with its own or shared k and g)
   // takes 263-266 us instead of 271-278 at config 4, from the write-back of
   // this kernel's output overlapping it in a different address order.  The
-  // walk advances with adds only: divisions in the loop pushed it into spills.
-  const uint32_t Hu = (uint32_t)H, Bu = (uint32_t)(tiles / (NT * H));
-  hl::DescWalk walk = hl::desc_walk_at(blockIdx.x, Bu, Hu);
-  const hl::DescWalk step = hl::desc_walk_at(gridDim.x, Bu, Hu);
+  // walk index is decomposed once per tile, on wave-uniform values.
+  const uint32_t Hu = (uint32_t)H, Bu = (uint32_t)(tiles / (NT * H)), ntiles = (uint32_t)tiles;
+  unsigned int* const ticket = &g_o_tiles[slot][0];
+  unsigned int* const finished = &g_o_tiles[slot][1];
   char* const lvb = reinterpret_cast<char*>(lv);
   char* const lhb = reinterpret_cast<char*>(lh);
   char* const lkb = reinterpret_cast<char*>(lk);
@@ -264,7 +281,8 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   u32x4 vr[C::kVLoads], hr[C::kHLoads], kr[C::kKLoads], qr[KS];
   float gr = 0.f;
   int64_t nx_hh = 0, nx_tok0 = 0;
-  auto prefetch = [&]() {  // the tile at `walk`
+  auto prefetch = [&](uint32_t t) {  // the tile at walk index t
+    const hl::DescWalk walk = hl::desc_walk_at(t, Bu, Hu);
     const int64_t c = (int64_t)NT - 1 - walk.cq;
     const int64_t hh = walk.hh, tile = ((int64_t)walk.b * NT + c) * H + hh;
     const int64_t tok0 = (int64_t)walk.b * T + c * 64;
@@ -309,21 +327,39 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     if (tid < kBT) gs[tid] = gr;
   };
 
-  int64_t t = blockIdx.x;
-  if (t >= tiles) return;  // whole workgroup
-  prefetch();
+  // Every workgroup, including one with no tile, counts itself finished; the
+  // last one resets the slot.  Its own ticket draws have returned before it
+  // counts (the wait on `pend`), so no draw of this launch follows the reset.
+  uint32_t pend = 0;  // thread 0: the ticket drawn for the tile after next
+  auto finish = [&]() {
+    if (tid == 0) {
+      asm volatile("" : : "v"(pend));
+      if (atomicAdd(finished, 1u) == gridDim.x - 1) {
+        atomicExch(ticket, 0u);
+        atomicExch(finished, 0u);
+      }
+    }
+  };
+  __shared__ uint32_t s_next;
+  uint32_t t = blockIdx.x;
+  if (t >= ntiles) {  // whole workgroup
+    finish();
+    return;
+  }
+  if (tid == 0) {
+    s_next = hl::dyn_tile(gridDim.x, atomicAdd(ticket, 1u));
+    pend = hl::dyn_tile(gridDim.x, atomicAdd(ticket, 1u));
+  }
+  prefetch(t);
   stage();
   lds_barrier();
+  uint32_t tn = __builtin_amdgcn_readfirstlane(s_next);  // the tile after t
   for (;;) {
     bf16x8 qh[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) qh[s] = __builtin_bit_cast(bf16x8, qr[s]);
-    const int64_t tn = t + gridDim.x;
     const int64_t hh = nx_hh, tok0 = nx_tok0;  // tile t
-    if (tn < tiles) {  // in flight while tile t computes
-      hl::desc_walk_step(walk, step, Bu, Hu);
-      prefetch();
-    }
+    if (tn < ntiles) prefetch(tn);  // in flight while tile t computes
 
     // Inter-chunk term, scaled by e^{g_i}.
     f32x4 acc[NB];
@@ -367,12 +403,18 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) store4(o + orow * V + 16 * nb + 4 * grp, acc[nb] * scale);
 
-    if (tn >= tiles) break;
+    if (tn >= ntiles) break;
     lds_barrier();  // every wave is done with tile t's LDS
     stage();
+    if (tid == 0) {  // s_next was read before the barrier above
+      s_next = pend;
+      pend = hl::dyn_tile(gridDim.x, atomicAdd(ticket, 1u));
+    }
     lds_barrier();
     t = tn;
+    tn = __builtin_amdgcn_readfirstlane(s_next);
   }
+  finish();
 }
 
 template <int K, int V>
@@ -380,9 +422,11 @@ hipError_t launch_o_pipe(const void* q, const void* k, const void* v, const void
                          void* o, float scale, int64_t B, int64_t T, int64_t H, int64_t grid,
                          hipStream_t s) {
   const int64_t NT = T / kBT;
+  static std::atomic<uint32_t> launches{0};
+  const uint32_t slot = launches.fetch_add(1, std::memory_order_relaxed) % kOTileSlots;
   hipLaunchKernelGGL((chunk_fwd_o_pipe_kernel<K, V>), dim3((unsigned)grid), dim3(kOThreads), 0, s,
                      (const bf16*)q, (const bf16*)k, (const bf16*)v, (const float*)g, (const float*)h,
-                     (bf16*)o, scale, T, H, NT, B * NT * H);
+                     (bf16*)o, scale, T, H, NT, B * NT * H, slot);
   return hipGetLastError();
 }
 

@@ -211,9 +211,11 @@ THM_HD constexpr int sout_col(int p, int cols) { return 4 * (p % (cols / 4)); }
 // chunk_fwd_o's pipelined kernel.
 //
 // Walk: sequence index t = cq (B H) + b H + hh visits tile (b, chunk
-// NT - 1 - cq, head hh): head fastest, chunks in descending order.  A
-// workgroup starts at t = its index and steps by the grid size G; the step
-// is desc_walk_at(G) added with carries, so the loop has no division.
+// NT - 1 - cq, head hh): head fastest, chunks in descending order.
+// Workgroups take walk indices dynamically: workgroup w first takes t = w,
+// then t = dyn_tile(G, n) for each ticket n = 0, 1, ... it draws from the
+// launch's counter (G = the grid size), until a t is past the end.  A
+// workgroup on a slower XCD so takes fewer tiles.
 struct DescWalk {
   uint32_t cq, b, hh;
 };
@@ -221,20 +223,7 @@ THM_HD inline DescWalk desc_walk_at(uint32_t t, uint32_t B, uint32_t H) {
   const uint32_t bh = B * H, cq = t / bh, r = t - cq * bh, b = r / H;
   return {cq, b, r - b * H};
 }
-// w += step (step.b < B and step.hh < H, as desc_walk_at gives).
-THM_HD inline void desc_walk_step(DescWalk& w, const DescWalk& step, uint32_t B, uint32_t H) {
-  w.hh += step.hh;
-  w.b += step.b;
-  w.cq += step.cq;
-  if (w.hh >= H) {
-    w.hh -= H;
-    ++w.b;
-  }
-  if (w.b >= B) {
-    w.b -= B;
-    ++w.cq;
-  }
-}
+THM_HD constexpr uint32_t dyn_tile(uint32_t grid, uint32_t ticket) { return grid + ticket; }
 // Loads of one tile, byte offsets = a per-lane part (loop-invariant, 32-bit)
 // plus a wave-uniform step per load `it` (256 threads):
 //   h [K x V] fp32: thread tid's load it is row tid / (V / 4) + it 256 / (V / 4),
