@@ -24,10 +24,10 @@
 //   3. acc[n][i] += sum_j v[j][n] P[i][j]: the P accumulator pairs are the B
 //      operand in paired order, v^T comes from LDS in the same order;
 //   4. o[i][n..n+3] = scale * acc.
-#include <atomic>
 #include <type_traits>
 
 #include "h_layout.h"
+#include "handout.h"
 #include "mfma.h"
 
 namespace thm {
@@ -203,22 +203,15 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
 // 16-byte row reads), which keeps the prefetched set to 28 16-byte loads per
 // thread.  The arithmetic is the kernel above's.
 //
-// The tiles are handed out at run time (h_layout.h dyn_tile): each workgroup
-// draws a ticket from a counter for the tile after next, one tile ahead of
-// need, so the atomic's latency stays hidden.  Workgroups on the XCDs that
-// run slower (XCDs 1 and 5 on every box measured) so take fewer tiles; the
-// fixed walk t, t + G, ... waited for them (419.4-419.9 against 400.1 us at
-// config 4, interleaved, o bit-identical).  The counters live in a static
-// device array of kOTileSlots slots, one per launch in rotation; the last
-// workgroup of a launch to finish resets its slot for the next use.  So up
-// to kOTileSlots launches may be in flight on one device at once (across
-// streams) before two of them could share a counter.
+// The tiles are handed out at run time (handout.h): workgroups on the XCDs
+// that run slower (XCDs 1 and 5 on every box measured) take fewer tiles; the
+// fixed walk t, t + G, ... waited for them (419.1-419.9 against 400.1-401.5
+// us alone at config 4, interleaved, o bit-identical).
 constexpr int kOPipeWGsPerCU = 2;
-constexpr int kOTileSlots = 256;
 
-// Slot s: {next ticket, workgroups finished}.  Device code uses it by name;
-// host code never passes its address (it passes the slot index).
-__device__ __align__(256) unsigned int g_o_tiles[kOTileSlots][2];
+// The hand-out counters of this kernel (handout.h): slot s = {next ticket,
+// workgroups finished}.
+__device__ __align__(256) unsigned int g_o_tiles[kTileSlots][2];
 
 template <int K, int V>
 struct OPCfg {
@@ -264,8 +257,7 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   // this kernel's output overlapping it in a different address order.  The
   // walk index is decomposed once per tile, on wave-uniform values.
   const uint32_t Hu = (uint32_t)H, Bu = (uint32_t)(tiles / (NT * H)), ntiles = (uint32_t)tiles;
-  unsigned int* const ticket = &g_o_tiles[slot][0];
-  unsigned int* const finished = &g_o_tiles[slot][1];
+  TileHandout ho(g_o_tiles[slot]);
   char* const lvb = reinterpret_cast<char*>(lv);
   char* const lhb = reinterpret_cast<char*>(lh);
   char* const lkb = reinterpret_cast<char*>(lk);
@@ -327,29 +319,13 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     if (tid < kBT) gs[tid] = gr;
   };
 
-  // Every workgroup, including one with no tile, counts itself finished; the
-  // last one resets the slot.  Its own ticket draws have returned before it
-  // counts (the wait on `pend`), so no draw of this launch follows the reset.
-  uint32_t pend = 0;  // thread 0: the ticket drawn for the tile after next
-  auto finish = [&]() {
-    if (tid == 0) {
-      asm volatile("" : : "v"(pend));
-      if (atomicAdd(finished, 1u) == gridDim.x - 1) {
-        atomicExch(ticket, 0u);
-        atomicExch(finished, 0u);
-      }
-    }
-  };
   __shared__ uint32_t s_next;
   uint32_t t = blockIdx.x;
   if (t >= ntiles) {  // whole workgroup
-    finish();
+    ho.finish(tid);
     return;
   }
-  if (tid == 0) {
-    s_next = hl::dyn_tile(gridDim.x, atomicAdd(ticket, 1u));
-    pend = hl::dyn_tile(gridDim.x, atomicAdd(ticket, 1u));
-  }
+  ho.start(&s_next, tid);
   prefetch(t);
   stage();
   lds_barrier();
@@ -406,15 +382,12 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     if (tn >= ntiles) break;
     lds_barrier();  // every wave is done with tile t's LDS
     stage();
-    if (tid == 0) {  // s_next was read before the barrier above
-      s_next = pend;
-      pend = hl::dyn_tile(gridDim.x, atomicAdd(ticket, 1u));
-    }
+    ho.advance(&s_next, tid);  // every thread read s_next before the barrier above
     lds_barrier();
     t = tn;
     tn = __builtin_amdgcn_readfirstlane(s_next);
   }
-  finish();
+  ho.finish(tid);
 }
 
 template <int K, int V>
@@ -422,8 +395,7 @@ hipError_t launch_o_pipe(const void* q, const void* k, const void* v, const void
                          void* o, float scale, int64_t B, int64_t T, int64_t H, int64_t grid,
                          hipStream_t s) {
   const int64_t NT = T / kBT;
-  static std::atomic<uint32_t> launches{0};
-  const uint32_t slot = launches.fetch_add(1, std::memory_order_relaxed) % kOTileSlots;
+  const uint32_t slot = next_tile_slot();
   hipLaunchKernelGGL((chunk_fwd_o_pipe_kernel<K, V>), dim3((unsigned)grid), dim3(kOThreads), 0, s,
                      (const bf16*)q, (const bf16*)k, (const bf16*)v, (const float*)g, (const float*)h,
                      (bf16*)o, scale, T, H, NT, B * NT * H, slot);
