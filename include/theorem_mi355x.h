@@ -157,6 +157,9 @@ int thm_chunk_fwd_h(const void* k, const void* w, const void* vu, const void* g,
  * factored form q*exp(g), v*exp(-g)).
  *   qkv_dtype: dtype of q, k, v and o (F32 or BF16). g and h are fp32.
  *   g may be NULL (no gate). K, V in {64, 128}; T % 64 == 0.
+ *   Allocates nothing.  Large bf16 grids take their tiles from counter slots
+ *   of a static device array (256 per device), one per launch in rotation:
+ *   at most 256 of these launches may be in flight on a device at once.
  */
 int thm_chunk_fwd_o(const void* q, const void* k, const void* v, const void* g,
                     const void* h, void* o, float scale,
