@@ -127,8 +127,8 @@ def test_o_pipelined_handout_across_launches_and_streams(dev):
     # for bit, and that output must match the oracle.
     K = V = 64
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    B, H = 1, 16
-    T = 64 * max(2, -(-4 * cus // H))  # at least 2 tiles per persistent workgroup
+    B, H = 1, 32
+    T = 64 * max(2, -(-6 * cus // H))  # 3 tiles per persistent workgroup (2 per CU)
     d = configs.make_o_inputs(B, T, H, K, V, seed=21, device=dev, dtype=torch.bfloat16)
     args = dict(q=d["q"], k=d["k"], v=d["v"], g=d["g"], h=d["h"], scale=d["scale"])
     o0 = chunk_fwd_o.custom_kernel(args)
@@ -150,6 +150,16 @@ def test_o_pipelined_handout_across_launches_and_streams(dev):
     sync()
     bad = [i for i, o in enumerate(outs) if not torch.equal(o, o0)]
     assert not bad, f"two-stream launches {bad} differ from the first"
+    # A smaller pipelined shape right after (2 tiles per workgroup instead of 3,
+    # the same slots).
+    H2 = H // 2
+    T2 = 64 * max(2, -(-4 * cus // H2))
+    assert B * (T2 // 64) * H2 < B * (T // 64) * H
+    d2 = configs.make_o_inputs(B, T2, H2, K, V, seed=22, device=dev, dtype=torch.bfloat16)
+    o2 = chunk_fwd_o.custom_kernel(dict(q=d2["q"], k=d2["k"], v=d2["v"], g=d2["g"], h=d2["h"], scale=d2["scale"]))
+    sync()
+    e2 = odn.chunk_fwd_o_diff(np_(d2["q"]), np_(d2["k"]), np_(d2["v"]), np_(d2["g"]), np_(d2["h"]), d2["scale"])
+    assert_close(o2, e2, 1e-2, 1e-2, "o pipelined, smaller shape after")
 
 
 def test_o_closed_forms(dev):
