@@ -18,7 +18,11 @@ fit in about 12 s) and scales to a full step. ``floors`` times memory-only
 kernels that move each step kernel's algorithmic bytes in its own tile pattern
 with no compute (theorem_amd/csrc/floors.hip): the fastest this box moves
 those bytes in that pattern, reported per kernel as ``floor_us`` and
-``of_floor`` (floor / kernel time) beside the 8 TB/s roofline.
+``of_floor`` (floor / kernel time) beside the 8 TB/s roofline.  Each floor
+also gives the same pattern with tiles of 2 and 4 adjacent heads
+(``heads2_us``, ``heads4_us``: 512 B and 1 KB contiguous row runs) and a
+contiguous ceiling, the kernel's read and write bytes as one contiguous
+stream each in the same ratio (``ceiling_us``; per kernel ``of_ceiling``).
 ``measured_peaks`` gives the box's copy rate and bf16 MFMA throughput (a
 register-only MFMA loop); each kernel's ``mfma_frac_of_measured`` is its flop
 rate against the latter. ``shapes`` gives each kernel's latency at configs
@@ -336,8 +340,31 @@ def pattern_floors(torch, inp, conv_in, reps: int = 5):
         "chunk_gated_delta_fwd": (lambda: lib.thm_floor_ho(P(q), P(k), P(w2), P(u2), P(g), P(o2), i64(B), i64(T),
                                                            i64(H), stream), N * (5 * 256 + 4)),
     }
-    out = {}
-    for name, (fn, by) in runs.items():
+    # Multi-head variants of the tile floors: tiles of 2 and 4 adjacent heads,
+    # so each token row of a tensor is one 512 B or 1 KB contiguous run.
+    heads = {
+        "recompute_w_u": lambda nh: lib.thm_floor_wu_heads(P(k), P(v), P(A), P(beta), P(g), P(w2), P(u2), i64(B),
+                                                           i64(T), i64(H), ctypes.c_int32(nh), stream),
+        "chunk_fwd_h": lambda nh: lib.thm_floor_h_heads(P(k), P(w2), P(u2), P(g), P(h2), P(vn2), i64(B), i64(T),
+                                                        i64(H), ctypes.c_int32(nh), stream),
+        "chunk_fwd_o": lambda nh: lib.thm_floor_o_heads(P(q), P(k), P(v), P(h2), P(g), P(o2), i64(B), i64(T), i64(H),
+                                                        ctypes.c_int32(nh), stream),
+    }
+    # Contiguous ceilings: each kernel's read and write bytes as one
+    # contiguous stream per direction, in the kernel's read : write ratio.
+    NC = N // 64
+    mix = {
+        "causal_conv1d": (x.numel() * x.element_size(), x.numel() * x.element_size()),
+        "recompute_w_u": (N * (3 * 256 + 8), N * 2 * 256),
+        "chunk_fwd_h": (N * (3 * 256 + 4), N * 256 + NC * 65536),
+        "chunk_fwd_o": (N * (3 * 256 + 4) + NC * 65536, N * 256),
+        "wy_fwd": (N * (2 * 256 + 8), N * 2 * 256),
+        "chunk_gated_delta_fwd": (N * (4 * 256 + 4), N * 256),
+    }
+    src = torch.empty(max(r for r, _ in mix.values()), dtype=torch.uint8, device=k.device)
+    dst = torch.empty(max(w for _, w in mix.values()), dtype=torch.uint8, device=k.device)
+
+    def best_of(fn):
         if fn() != 0:
             return None
         torch.cuda.synchronize()
@@ -349,7 +376,25 @@ def pattern_floors(torch, inp, conv_in, reps: int = 5):
             e1.record()
             torch.cuda.synchronize()
             best = min(best, e0.elapsed_time(e1) * 1e3)
+        return best
+
+    out = {}
+    for name, (fn, by) in runs.items():
+        best = best_of(fn)
+        if best is None:
+            return None
         out[name] = {"us": round(best, 2), "bytes": by, "GBps": round(by / best / 1e3, 1)}
+        for nh in (2, 4):
+            if name in heads and H % nh == 0:
+                t = best_of(lambda: heads[name](nh))
+                if t is not None:
+                    out[name][f"heads{nh}_us"] = round(t, 2)
+        rd, wr = mix[name]
+        t = best_of(lambda: lib.thm_floor_mix(P(src), i64(rd), P(dst), i64(wr), stream))
+        if t is not None:
+            out[name]["ceiling_us"] = round(t, 2)
+            out[name]["ceiling_GBps"] = round((rd + wr) / t / 1e3, 1)
+    del src, dst
     return out
 
 
@@ -731,6 +776,9 @@ def main() -> int:
             for n in names:
                 kernels[n]["floor_us"] = floors[n]["us"]
                 kernels[n]["of_floor"] = round(floors[n]["us"] / kernels[n]["us"], 3)
+                if "ceiling_us" in floors[n]:
+                    kernels[n]["ceiling_us"] = floors[n]["ceiling_us"]
+                    kernels[n]["of_ceiling"] = round(floors[n]["ceiling_us"] / kernels[n]["us"], 3)
         print("[bench] measured peaks (copy, bf16 MFMA)", file=sys.stderr, flush=True)
         peaks = measured_peaks(torch, inp["k"].device, floors)
         if peaks:
@@ -752,6 +800,9 @@ def main() -> int:
             if floors and n in floors and n in ext:
                 ext[n]["floor_us"] = floors[n]["us"]
                 ext[n]["of_floor"] = round(floors[n]["us"] / ext[n]["us"], 3)
+                if "ceiling_us" in floors[n]:
+                    ext[n]["ceiling_us"] = floors[n]["ceiling_us"]
+                    ext[n]["of_ceiling"] = round(floors[n]["ceiling_us"] / ext[n]["us"], 3)
 
     cpu = None
     if not args.no_cpu:

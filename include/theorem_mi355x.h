@@ -157,9 +157,16 @@ int thm_chunk_fwd_h(const void* k, const void* w, const void* vu, const void* g,
  * factored form q*exp(g), v*exp(-g)).
  *   qkv_dtype: dtype of q, k, v and o (F32 or BF16). g and h are fp32.
  *   g may be NULL (no gate). K, V in {64, 128}; T % 64 == 0.
- *   Allocates nothing.  Large bf16 grids take their tiles from counter slots
- *   of a static device array (256 per device), one per launch in rotation:
- *   at most 256 of these launches may be in flight on a device at once.
+ *   Allocates nothing.  Large bf16 grids (at least twice as many tiles as
+ *   2 workgroups per CU) hand their tiles out at run time from counter slots
+ *   of a static device array (256 per device), which each launch resets.
+ *   The host gives a slot only to a launch whose slot's previous launch has
+ *   completed (an event per slot, recorded behind each launch), so launches
+ *   in flight on any streams never share one; with every slot busy, a launch
+ *   takes the fixed walk of its tiles.  A launch on a stream that is being
+ *   captured into a graph always takes the fixed walk and touches no counter:
+ *   the captured graph holds no state and may be replayed any number of
+ *   times, on any streams.  Outputs are the same on either walk.
  */
 int thm_chunk_fwd_o(const void* q, const void* k, const void* v, const void* g,
                     const void* h, void* o, float scale,

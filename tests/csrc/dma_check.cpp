@@ -30,7 +30,10 @@
 //     reads and form_L's row reads, all conflict-free;
 //   * chunk_fwd_o's pipelined kernel: its walk (desc_walk_at) maps walk
 //     indices to tiles one to one, in descending chunk order; its run-time
-//     hand-out of walk indices (dyn_tile) processes each exactly once; and its
+//     hand-out of walk indices (handout.h HandoutCore, driven here through
+//     interleaved workgroups) processes each exactly once, resets its slot
+//     for the next launch, and so does the fixed walk; two launches sharing
+//     one slot do not (which the host's slot table prevents); and its
 //     load offsets (o_*_lane /
 //     o_*_step) read exactly the elements its staging writes, in bounds and
 //     in 32 bits up to the entry point's limit on H.
@@ -44,6 +47,7 @@
 #include <vector>
 
 #include "h_layout.h"
+#include "handout.h"
 #include "pipe_cfg.h"
 
 using namespace thm;
@@ -766,6 +770,80 @@ static void check_xcd_tile_order() {
     }
 }
 
+// The run-time hand-out (handout.h HandoutCore, the kernel's own protocol
+// code) replayed on the host: each workgroup runs the pipelined kernel's
+// control flow -- take walk index wg (or stop at once if wg is past the end),
+// start(), then per tile: process it, stop if the next index is past the
+// end, else advance() -- and finish() at its end.  The workgroups of
+// `launches` launches sharing `slot` (null: the fixed walk) take steps in a
+// pseudo-random interleaving; each launch's count of processings per walk
+// index is returned.  Every workgroup must stop, and exactly one finish() per
+// launch must report the reset.
+struct HostAtomics {
+  static unsigned int add(unsigned int* p, unsigned int v) {
+    const unsigned int old = *p;
+    *p = old + v;
+    return old;
+  }
+  static void exch(unsigned int* p, unsigned int v) { *p = v; }
+  static void wait(uint32_t) {}
+};
+
+static std::vector<std::vector<int>> replay_handout_shared(unsigned int* slot, uint32_t tiles, uint32_t G,
+                                                           int launches, uint32_t seed) {
+  struct Wg {
+    HandoutCore<HostAtomics> core;
+    int launch;
+    uint32_t wg, t, tn;
+    int state;  // 0 not started, 1 running, 2 stopped
+  };
+  std::vector<Wg> wgs;
+  for (int l = 0; l < launches; ++l)
+    for (uint32_t w = 0; w < G; ++w) wgs.push_back({HandoutCore<HostAtomics>(slot, G), l, w, w, 0, 0});
+  std::vector<std::vector<int>> done(launches, std::vector<int>(tiles, 0));
+  std::vector<int> resets(launches, 0);
+  uint32_t lcg = seed * 2654435761u + 12345u;
+  const long limit = 4L * launches * (tiles + G) + 64;
+  for (long steps = 0;; ++steps) {
+    std::vector<size_t> live;
+    for (size_t i = 0; i < wgs.size(); ++i)
+      if (wgs[i].state != 2) live.push_back(i);
+    if (live.empty()) break;
+    CHECK(steps < limit, "o hand-out tiles=%u G=%u: does not stop", tiles, G);
+    if (steps >= limit) break;
+    lcg = lcg * 1664525u + 1013904223u;
+    Wg& x = wgs[live[(lcg >> 8) % live.size()]];
+    if (x.state == 0) {
+      if (x.wg >= tiles) {
+        resets[x.launch] += x.core.finish();
+        x.state = 2;
+        continue;
+      }
+      x.t = x.wg;
+      x.tn = x.core.start(x.wg);
+      x.state = 1;
+      continue;
+    }
+    CHECK(x.t < tiles, "o hand-out: walk index %u past the end processed", x.t);
+    if (x.t < tiles) ++done[x.launch][x.t];
+    if (x.tn >= tiles) {
+      resets[x.launch] += x.core.finish();
+      x.state = 2;
+      continue;
+    }
+    const uint32_t nn = x.core.advance();
+    x.t = x.tn;
+    x.tn = nn;
+  }
+  if (slot && launches == 1)
+    CHECK(resets[0] == 1, "o hand-out tiles=%u G=%u: %d workgroups reset the slot", tiles, G, resets[0]);
+  return done;
+}
+
+static std::vector<int> replay_handout(unsigned int* slot, uint32_t tiles, uint32_t G, uint32_t seed) {
+  return replay_handout_shared(slot, tiles, G, 1, seed)[0];
+}
+
 // chunk_fwd_o's pipelined kernel: workgroup wg of G visits sequence indices
 // wg, wg + G, ... < B NT H, advancing a DescWalk by desc_walk_at(G).
 static void check_o_walk() {
@@ -788,52 +866,34 @@ static void check_o_walk() {
     }
     for (uint32_t tile = 0; tile < tiles; ++tile)
       CHECK(seen[tile] == 1, "o walk B=%u H=%u NT=%u: tile %u at %d walk indices", c.B, c.H, c.NT, tile, seen[tile]);
-    // The run-time hand-out, replayed with the workgroups drawing tickets in
-    // several interleavings: workgroup w takes w (if w < tiles), draws the
-    // tickets of the next two tiles, then per tile processed one more; it
-    // stops at the first tile index past the end.  Every walk index must be
-    // processed exactly once, every workgroup must stop, and a draw it drops
-    // must be past the end.
     for (uint32_t seed = 1; seed <= 3; ++seed) {
-      struct Wg {
-        uint32_t t, tn, pend;
-        bool live;
-      };
-      std::vector<Wg> wg(c.G);
-      std::vector<int> done(tiles, 0);
-      uint32_t counter = 0, lcg = seed * 2654435761u;
-      auto draw = [&]() { return hl::dyn_tile(c.G, counter++); };
-      for (uint32_t w = 0; w < c.G; ++w) {
-        wg[w].live = w < tiles;
-        if (!wg[w].live) continue;
-        wg[w].t = w;
-        wg[w].tn = draw();
-        wg[w].pend = draw();
+      // Three launches in a row on one slot (its reuse), then the fixed walk.
+      unsigned int slot[2] = {0, 0};
+      for (int launch = 0; launch < 3; ++launch) {
+        const std::vector<int> done = replay_handout(slot, tiles, c.G, seed * 7 + launch);
+        for (uint32_t t = 0; t < tiles; ++t)
+          CHECK(done[t] == 1, "o hand-out B=%u H=%u NT=%u G=%u seed %u launch %d: walk index %u processed %d times",
+                c.B, c.H, c.NT, c.G, seed, launch, t, done[t]);
+        CHECK(slot[0] == 0 && slot[1] == 0, "o hand-out G=%u launch %d: slot {%u, %u} not reset at the end", c.G,
+              launch, slot[0], slot[1]);
       }
-      for (long steps = 0;; ++steps) {
-        std::vector<uint32_t> live;
-        for (uint32_t w = 0; w < c.G; ++w)
-          if (wg[w].live) live.push_back(w);
-        if (live.empty()) break;
-        CHECK(steps < 4L * (tiles + c.G) + 16, "o hand-out B=%u H=%u NT=%u G=%u: does not stop", c.B, c.H, c.NT, c.G);
-        if (steps >= 4L * (tiles + c.G) + 16) break;
-        lcg = lcg * 1664525u + 1013904223u;
-        Wg& x = wg[live[(lcg >> 8) % live.size()]];
-        CHECK(x.t < tiles, "o hand-out: tile %u past the end processed", x.t);
-        if (x.t < tiles) ++done[x.t];
-        if (x.tn >= tiles) {
-          CHECK(x.pend >= tiles, "o hand-out: a dropped draw %u is a tile", x.pend);
-          x.live = false;
-          continue;
-        }
-        x.t = x.tn;
-        x.tn = x.pend;
-        x.pend = draw();
-      }
+      const std::vector<int> fixed = replay_handout(nullptr, tiles, c.G, seed);
       for (uint32_t t = 0; t < tiles; ++t)
-        CHECK(done[t] == 1, "o hand-out B=%u H=%u NT=%u G=%u seed %u: walk index %u processed %d times", c.B, c.H,
-              c.NT, c.G, seed, t, done[t]);
+        CHECK(fixed[t] == 1, "o fixed walk B=%u H=%u NT=%u G=%u: walk index %u processed %d times", c.B, c.H, c.NT,
+              c.G, t, fixed[t]);
     }
+  }
+  // Two launches in flight on one slot (what the host's slot table rules
+  // out): their draws interleave on one counter, so tiles are skipped or
+  // repeated.  The replay must show it.
+  {
+    unsigned int slot[2] = {0, 0};
+    const uint32_t tiles = 2 * 16 * 32, G = 64;
+    const std::vector<std::vector<int>> done = replay_handout_shared(slot, tiles, G, 2, 5);
+    bool wrong = false;
+    for (const auto& d : done)
+      for (uint32_t t = 0; t < tiles; ++t) wrong |= d[t] != 1;
+    CHECK(wrong, "o hand-out: two launches sharing a slot processed every tile once (the replay sees no sharing)");
   }
 }
 

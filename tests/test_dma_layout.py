@@ -136,6 +136,14 @@ MUTATIONS = [
     ("h_layout.h", "THM_HD constexpr uint32_t dyn_tile(uint32_t grid, uint32_t ticket) { return grid + ticket; }",
      "THM_HD constexpr uint32_t dyn_tile(uint32_t grid, uint32_t ticket) { return grid + ticket + 1; }",
      "chunk_fwd_o hand-out: a tile skipped"),
+    ("handout.h", "if (Ops::add(finished, 1u) == grid - 1) {", "if (Ops::add(finished, 1u) == grid - 2) {",
+     "chunk_fwd_o hand-out: slot reset before the last workgroup is done"),
+    ("handout.h", "    const uint32_t n = draw(wg);\n    pend = draw(n);", "    const uint32_t n = draw(wg);\n    pend = n;",
+     "chunk_fwd_o hand-out: start draws one ticket for two tiles"),
+    ("handout.h", ": prev + grid; }", ": prev + grid + 1; }",
+     "chunk_fwd_o fixed walk (graph capture): a stride past G skips tiles"),
+    ("handout.h", "      Ops::exch(finished, 0u);\n", "",
+     "chunk_fwd_o hand-out: finished count not reset for the slot's next launch"),
     ("h_layout.h", "(uint32_t)(tid % (n / 8)) * 8u) * 2u;", "(uint32_t)(tid % (n / 8)) * 4u) * 2u;",
      "chunk_fwd_o: v / k lane offset at half the element stride"),
     ("h_layout.h", "return (int64_t)it * (256 / (V / 4)) * V * 4; }", "return (int64_t)it * (256 / (V / 4)) * V * 2; }",
@@ -149,7 +157,7 @@ def test_dma_layout_check_catches_planted_slip(tmp_path, header, old, new, what)
     assert text.count(old) == 1, f"mutation site not found in {header}: {old}"
     mut = tmp_path / "mut"
     mut.mkdir()
-    for h in ("h_layout.h", "pipe_cfg.h"):
+    for h in ("h_layout.h", "pipe_cfg.h", "handout.h"):
         (mut / h).write_text((CSRC / h).read_text())
     (mut / header).write_text(text.replace(old, new))
     r = _build_and_run(tmp_path, include_first=mut)

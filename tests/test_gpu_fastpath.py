@@ -99,3 +99,33 @@ def test_fastpath_declines_outside_common_case(dev):
         chunk_fwd_o.custom_kernel(dict(data, h=d["h"].half()))
     x, w, b = configs.make_conv_inputs(1, 64, 100, 4, seed=6, device=dev)
     assert fp.conv1d(x.transpose(1, 2).contiguous().transpose(1, 2), w, b, 0) is None
+
+
+def test_fastpath_raises_host_rejection_once(dev, monkeypatch):
+    """An argument the fast path's checks pass but the C ABI rejects on the
+    host (an unsupported K or W): the C status comes back from the fast path
+    and the wrapper raises ValueError at once, without entering its ctypes
+    path (which would validate and call the C ABI a second time)."""
+    assert _capi.fastpath() is not None
+
+    def no_ctypes_path(*a, **k):
+        raise AssertionError("the ctypes path ran after the fast path's status")
+
+    monkeypatch.setattr(_capi, "dev_ptrs", no_ctypes_path)
+    monkeypatch.setattr(_capi, "require_device", no_ctypes_path)
+    d = configs.make_o_inputs(1, 128, 2, 64, 64, seed=7, device=dev)
+    q = d["q"][..., :32].contiguous()
+    k = d["k"][..., :32].contiguous()
+    h = d["h"][:, :, :, :32].contiguous()
+    with pytest.raises(ValueError, match="thm_chunk_fwd_o"):
+        chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=d["v"], g=d["g"], h=h, scale=d["scale"]))
+    with pytest.raises(ValueError, match="thm_chunk_fwd_h"):
+        chunk_fwd_h.custom_kernel(dict(k=k, v=d["v"], g=d["g"]))
+    wd = configs.make_wu_inputs(1, 128, 2, 64, 64, seed=8, device=dev)
+    with pytest.raises(ValueError, match="thm_recompute_w_u_fwd"):
+        recompute_w_u.custom_kernel(recompute_w_u.Data(**dict(wd, k=wd["k"][..., :32].contiguous()),
+                                                       B=1, T=128, H=2, K=32, V=64))
+    x, w, b = configs.make_conv_inputs(1, 64, 100, 4, seed=9, device=dev)
+    w9 = torch.zeros(64, 9, dtype=w.dtype, device=dev)
+    with pytest.raises(ValueError, match="thm_causal_conv1d_fwd"):
+        causal_conv1d.custom_kernel((x, w9, b))

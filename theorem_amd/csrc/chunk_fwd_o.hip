@@ -213,6 +213,13 @@ constexpr int kOPipeWGsPerCU = 2;
 // workgroups finished}.
 __device__ __align__(256) unsigned int g_o_tiles[kTileSlots][2];
 
+// The host side of those slots (handout.h TileSlots): one table for every
+// instantiation of the kernel, since they share g_o_tiles.
+TileSlots& o_tile_slots() {
+  static TileSlots slots;
+  return slots;
+}
+
 template <int K, int V>
 struct OPCfg {
   static constexpr int kPitchB = hl::tr_pitch(V * 2);    // bytes per v / h row (layouts as in OCfg)
@@ -257,7 +264,7 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   // this kernel's output overlapping it in a different address order.  The
   // walk index is decomposed once per tile, on wave-uniform values.
   const uint32_t Hu = (uint32_t)H, Bu = (uint32_t)(tiles / (NT * H)), ntiles = (uint32_t)tiles;
-  TileHandout ho(g_o_tiles[slot]);
+  TileHandout ho(g_o_tiles, slot);
   char* const lvb = reinterpret_cast<char*>(lv);
   char* const lhb = reinterpret_cast<char*>(lh);
   char* const lkb = reinterpret_cast<char*>(lk);
@@ -395,11 +402,14 @@ hipError_t launch_o_pipe(const void* q, const void* k, const void* v, const void
                          void* o, float scale, int64_t B, int64_t T, int64_t H, int64_t grid,
                          hipStream_t s) {
   const int64_t NT = T / kBT;
-  const uint32_t slot = next_tile_slot();
+  TileSlots& slots = o_tile_slots();
+  const uint32_t slot = slots.acquire(s);
   hipLaunchKernelGGL((chunk_fwd_o_pipe_kernel<K, V>), dim3((unsigned)grid), dim3(kOThreads), 0, s,
                      (const bf16*)q, (const bf16*)k, (const bf16*)v, (const float*)g, (const float*)h,
                      (bf16*)o, scale, T, H, NT, B * NT * H, slot);
-  return hipGetLastError();
+  const hipError_t e = hipGetLastError();
+  slots.release(slot, s, e == hipSuccess);
+  return e;
 }
 
 // ---------------------------------------------------------------------------

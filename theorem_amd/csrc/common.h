@@ -60,6 +60,18 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Wave-scope LDS hand-off between lanes of one wavefront: LDS writes of some
+// lanes before it are visible to LDS reads of other lanes after it.  The wave
+// executes its LDS instructions in order, so this emits no instruction; the
+// fences and the wave barrier stop the compiler from moving an LDS read of
+// one lane's data above another lane's write (which it may do when it can
+// prove the two addresses of one lane differ).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 // Head index and first token row of tile `tile` of a [B, T / 64, H] tile
 // grid with the head fastest.  Every entry point that uses it checks that the
 // tile count is below 2^31, so 32-bit unsigned division is exact; it replaces

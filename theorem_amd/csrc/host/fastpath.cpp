@@ -5,11 +5,13 @@
 //
 // It is an accelerator only.  Each function handles the common case (every
 // tensor on one GPU, dense row-major, 16-byte aligned, the dtypes and shapes
-// the kernels take) and returns None for anything else, or when the C ABI
-// returns a nonzero status; the Python wrapper then runs its own path, which
-// raises the reference's errors.  The kernels, their arguments and the
-// outputs' allocation (torch's caching allocator, the current stream) are the
-// same on both paths.
+// the kernels take) and returns None for anything else; the Python wrapper
+// then runs its own path, which raises the reference's errors.  When the C
+// ABI returns a nonzero status, the function returns that status (an int)
+// and the wrapper raises it at once (ValueError for an argument the C side
+// rejected, RuntimeError for a launch error), with no second attempt.  The
+// kernels, their arguments and the outputs' allocation (torch's caching
+// allocator, the current stream) are the same on both paths.
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
 
@@ -53,7 +55,7 @@ py::object conv1d(const at::Tensor& x, const at::Tensor& weight, const c10::opti
   at::Tensor out = at::empty_like(x);
   const int st = thm_causal_conv1d_fwd(x.data_ptr(), weight.data_ptr(), ptr(bias), out.data_ptr(), B, D, S,
                                        (int32_t)W, xd, wd, activation, stream_of(dev));
-  if (st != THM_OK) return py::none();
+  if (st != THM_OK) return py::int_(st);
   return py::cast(out);
 }
 
@@ -77,7 +79,7 @@ py::object wu(const at::Tensor& k, const at::Tensor& v, const at::Tensor& beta, 
   const int st = thm_recompute_w_u_fwd(k.data_ptr(), v.data_ptr(), beta.data_ptr(), A.data_ptr(), ptr(g),
                                        w.data_ptr(), u.data_ptr(), B, T, H, K, V, (int32_t)kBT, code,
                                        stream_of(dev));
-  if (st != THM_OK) return py::none();
+  if (st != THM_OK) return py::int_(st);
   return py::make_tuple(w, u);
 }
 
@@ -106,7 +108,7 @@ py::object h(const at::Tensor& k, const c10::optional<at::Tensor>& w, const at::
   const int st = thm_chunk_fwd_h(k.data_ptr(), ptr(w), vu.data_ptr(), ptr(g), ptr(h0), hs.data_ptr(),
                                  vn.has_value() ? vn->data_ptr() : nullptr, ht.has_value() ? ht->data_ptr() : nullptr,
                                  B, T, H, K, V, (int32_t)kBT, code, delta ? THM_H_DELTA : 0, stream_of(dev));
-  if (st != THM_OK) return py::none();
+  if (st != THM_OK) return py::int_(st);
   return py::make_tuple(hs, vn.has_value() ? py::cast(*vn) : py::none(), ht.has_value() ? py::cast(*ht) : py::none());
 }
 
@@ -129,14 +131,14 @@ py::object o(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, cons
   at::Tensor out = at::empty_like(v);
   const int st = thm_chunk_fwd_o(q.data_ptr(), k.data_ptr(), v.data_ptr(), ptr(g), hs.data_ptr(), out.data_ptr(),
                                  (float)scale, B, T, H, K, V, (int32_t)kBT, code, stream_of(dev));
-  if (st != THM_OK) return py::none();
+  if (st != THM_OK) return py::int_(st);
   return py::cast(out);
 }
 
 }  // namespace
 
 PYBIND11_MODULE(_fastpath, m) {
-  m.doc() = "Host fast path of the custom_kernel wrappers (None: use the Python path)";
+  m.doc() = "Host fast path of the custom_kernel wrappers (None: use the Python path; int: C status to raise)";
   m.def("conv1d", &conv1d, py::arg("x"), py::arg("weight"), py::arg("bias"), py::arg("activation"));
   m.def("wu", &wu, py::arg("k"), py::arg("v"), py::arg("beta"), py::arg("A"), py::arg("g"));
   m.def("h", &h, py::arg("k"), py::arg("w"), py::arg("vu"), py::arg("g"), py::arg("h0"), py::arg("delta"),

@@ -109,7 +109,9 @@ __device__ __forceinline__ void invert_L(const float* Lb, float* Xb, float* Tb, 
   lds_barrier();
   // Column j of X is wave j's alone: X_ij needs X_mj (m < i, this wave's own
   // earlier blocks), the L blocks and X_ii (both behind the barrier above), so
-  // the levels need no barrier; LDS accesses of one wave complete in order.
+  // the levels need no workgroup barrier.  Each block a wave writes (T, then
+  // X_ij) is read back by other lanes of the same wave, so every write is
+  // followed by a wave-scope sync.
 #pragma unroll
   for (int d = 1; d < 4; ++d) {
     const int j = wv, i = wv + d;
@@ -121,8 +123,10 @@ __device__ __forceinline__ void invert_L(const float* Lb, float* Xb, float* Tb, 
         if (mm < i) acc = block_mm(Lb + blk(i, mm) * kBlk, Xb + blk(mm, j) * kBlk, acc);
       }
       block_put(Tb + wv * kBlk, acc, 1.f);
+      wave_lds_sync();
       acc = block_mm(Xb + blk(i, i) * kBlk, Tb + wv * kBlk, zero4());
       block_put(Xb + blk(i, j) * kBlk, acc, -1.f);
+      wave_lds_sync();
     }
   }
   lds_barrier();

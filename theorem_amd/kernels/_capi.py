@@ -92,7 +92,8 @@ def fastpath():
     built by theorem_amd.build: argument checks, output allocation and the C-ABI
     launch of a call in C++), or None when it is not built or does not load.
     Its functions return None for any call outside the common case; the
-    wrappers then take their ctypes path to the same kernels."""
+    wrappers then take their ctypes path to the same kernels.  A nonzero C
+    status comes back as an int, which the wrappers raise (``fast_result``)."""
     global _fast
     if _fast is None:
         _fast = False
@@ -113,6 +114,15 @@ def fastpath():
         except (ImportError, OSError):
             _fast = False
     return _fast or None
+
+
+def fast_result(r, what: str):
+    """A fast-path function's result: None (take the Python path), an int
+    (the C ABI's nonzero status: raised here, nothing is launched again) or
+    the outputs."""
+    if isinstance(r, int):
+        check(r, what)
+    return r
 
 
 def status_string(status: int) -> str:

@@ -60,7 +60,7 @@ def custom_kernel(data: tuple, activation: str | None = None) -> torch.Tensor:
     act = _ACT.get(activation)
     fp = _capi.fastpath() if act is not None else None
     if fp is not None:
-        out = fp.conv1d(x, weight, bias, act)
+        out = _capi.fast_result(fp.conv1d(x, weight, bias, act), "thm_causal_conv1d_fwd")
         if out is not None:
             return out
     B, D, S = x.shape

@@ -41,7 +41,7 @@ def custom_kernel(data):
             raise AssertionError(f"data[{key!r}]={data[key]} disagrees with the tensors ({val})")
     fp = _capi.fastpath()
     if fp is not None:
-        r = fp.h(k, w, vu, g, h0, delta, want_vn, want_ht)
+        r = _capi.fast_result(fp.h(k, w, vu, g, h0, delta, want_vn, want_ht), "thm_chunk_fwd_h")
         if r is not None:
             if delta:
                 return r

@@ -24,7 +24,7 @@ def custom_kernel(data: Dict[str, Any]) -> torch.Tensor:
     scale = float(data["scale"])
     fp = _capi.fastpath()
     if fp is not None:
-        o = fp.o(q, k, v, g, h, scale)
+        o = _capi.fast_result(fp.o(q, k, v, g, h, scale), "thm_chunk_fwd_o")
         if o is not None:
             return o
     B, T, H, K = q.shape

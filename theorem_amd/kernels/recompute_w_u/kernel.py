@@ -40,7 +40,7 @@ SHAPE_CONFIGS = {
 def _launch(k, v, beta, A, g):
     fp = _capi.fastpath()
     if fp is not None:
-        r = fp.wu(k, v, beta, A, g)
+        r = _capi.fast_result(fp.wu(k, v, beta, A, g), "thm_recompute_w_u_fwd")
         if r is not None:
             return r
     B, T, H, K = k.shape
