@@ -115,6 +115,19 @@ THM_HD constexpr uint32_t xtr_frag_off(int k0, int half, int c0, int lane, int r
   return xtile_off(k0 + 8 * (lane >> 4) + 4 * half + ((lane & 15) >> 2), c0 + 4 * (lane & 3), row_bytes);
 }
 
+// recompute_w_u's output staging tile: 64 token rows of row_bytes = n eb
+// (128, 256 or 512 bytes: 64 or 128 features, bf16 or fp32), unpadded.  The
+// MFMA result of a lane is 4 consecutive features of one token, written as
+// one 8-byte (bf16) or 16-byte (fp32) piece; a 32-lane pass writes 16 rows
+// at one logical 16-byte chunk.  Logical chunk q of row r sits at q ^ oswz(r),
+// which puts those 16 rows on 16 distinct chunks of the 256-byte bank window
+// (for 128-byte rows, two rows per window: 8 chunk positions x 2 halves).
+// The global stores read whole 16-byte chunks of consecutive rows back.
+THM_HD constexpr int oswz(int r, int row_bytes) { return row_bytes >= 256 ? (r & 15) : ((r >> 1) & 7); }
+THM_HD constexpr uint32_t otile_off(int r, int byte, int row_bytes) {
+  return (uint32_t)(r * row_bytes + ((((byte >> 4) ^ oswz(r, row_bytes))) << 4) + (byte & 15));
+}
+
 // chunk_fwd_o's register-staged v, h and k tiles are padded instead of
 // swizzled: a fragment address is then one per-lane base plus a constant,
 // folded into the LDS instruction's offset field, where an XOR swizzle needs

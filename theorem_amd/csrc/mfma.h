@@ -132,6 +132,15 @@ __device__ __forceinline__ void store4(bf16* p, f32x4 v) {
   *reinterpret_cast<bf16x4*>(p) = r;
 }
 
+// Write 4 consecutive outputs to LDS in the output dtype (the type of the
+// unused tag pointer), rounded as store4 rounds them.
+__device__ __forceinline__ void lds_store4(char* p, f32x4 v, const float*) { *reinterpret_cast<f32x4*>(p) = v; }
+__device__ __forceinline__ void lds_store4(char* p, f32x4 v, const bf16*) {
+  bf16x4 r;
+  r[0] = (bf16)v[0]; r[1] = (bf16)v[1]; r[2] = (bf16)v[2]; r[3] = (bf16)v[3];
+  *reinterpret_cast<bf16x4*>(p) = r;
+}
+
 // Write 4 (fp32 -> bf16 hi[, lo]) values to LDS.
 __device__ __forceinline__ void lds_put4(bf16* hi, bf16* lo, const float* v, bool with_lo) {
   bf16x4 h, l;
