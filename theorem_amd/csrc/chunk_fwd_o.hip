@@ -29,6 +29,7 @@
 #include "h_layout.h"
 #include "handout.h"
 #include "mfma.h"
+#include "vmem.h"
 
 namespace thm {
 namespace {
@@ -184,9 +185,12 @@ chunk_fwd_o_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k, const
     for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16x16x32(v_frag<C::kPitchB>(vhi, s, nb, lane), ph, acc[nb]);
   }
 
-  // 6. o[i][16 nb + 4 grp + 0..3].
+  // 6. o[i][16 nb + 4 grp + 0..3], as 16-byte pieces of 8 consecutive
+  // columns (vmem.h acc_pair_to_b128).
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) store4(o + qrow * V + 16 * nb + 4 * grp, acc[nb] * scale);
+  for (int m = 0; m < NB / 2; ++m)
+    *reinterpret_cast<u32x4*>(o + qrow * V + 32 * m + pair_col(grp)) =
+        acc_pair_to_b128(acc[2 * m] * scale, acc[2 * m + 1] * scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -384,7 +388,9 @@ chunk_fwd_o_pipe_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
     }
     const int64_t orow = (tok0 + i) * H + hh;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) store4(o + orow * V + 16 * nb + 4 * grp, acc[nb] * scale);
+    for (int m = 0; m < NB / 2; ++m)
+      *reinterpret_cast<u32x4*>(o + orow * V + 32 * m + pair_col(grp)) =
+          acc_pair_to_b128(acc[2 * m] * scale, acc[2 * m + 1] * scale);
 
     if (tn >= ntiles) break;
     lds_barrier();  // every wave is done with tile t's LDS

@@ -155,4 +155,29 @@ __device__ __forceinline__ u32x2 acc_to_row_quads_bf16(f32x4 v) {
   return r;
 }
 
+// Two accumulator tiles of one output row, columns 32 m + 4 grp .. + 3 (lo)
+// and 32 m + 16 + 4 grp .. + 3 (hi) of this lane (grp = lane / 16), as bf16
+// with 16 bytes per lane: lanes grp and grp ^ 1 (16 lanes apart) exchange one
+// tile each, so lane grp holds the 8 consecutive columns
+// 32 m + pair_col(grp) .. + 7, and the 4 lanes of a row cover 64 contiguous
+// bytes.  (Storing lo and hi as 8-byte pieces puts 32-byte runs of 16 rows in
+// one store instruction, which the memory path takes far more slowly.)
+__device__ __forceinline__ constexpr int pair_col(int grp) { return 8 * (grp >> 1) + 16 * (grp & 1); }
+__device__ __forceinline__ u32x4 acc_pair_to_b128(f32x4 lo, f32x4 hi) {
+  const int l = lane_id();
+  const bool odd = (l >> 4) & 1;
+  const f32x4 send = odd ? lo : hi, keep = odd ? hi : lo;
+  bf16x4 sb, kb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    sb[i] = (bf16)send[i];
+    kb[i] = (bf16)keep[i];
+  }
+  const u32x2 sp = __builtin_bit_cast(u32x2, sb), kp = __builtin_bit_cast(u32x2, kb);
+  const int src = (l ^ 16) * 4;
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)sp[0]);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)sp[1]);
+  return odd ? u32x4{r0, r1, kp[0], kp[1]} : u32x4{kp[0], kp[1], r0, r1};
+}
+
 }  // namespace thm
