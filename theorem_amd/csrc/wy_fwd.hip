@@ -18,12 +18,14 @@
 //   5. barrier; the [k | v] tile is staged in LDS over the inversion's blocks;
 //      barrier;
 //   6. D[n][t] = sum_j X[j][n] A'[t][j] on v_mfma_f32_16x16x32_bf16 (X^T
-//      fragments by ds_read_b64_tr_b16), one 8-byte bf16 store per lane.
+//      fragments by ds_read_b64_tr_b16), stored as 16-byte pieces of 8
+//      features after a lane-pair exchange.
 // A is the same fp32 value the A-builder writes, and the products are
 // recompute_w_u's, so w and u equal the two-kernel path's bit for bit.
 // bf16 inputs only.  HBM traffic per tile: k, v, beta, g read once, w, u
 // written once.
 #include "h_layout.h"
+#include "vmem.h"
 #include "wy_blocks.h"
 
 namespace thm {
@@ -80,29 +82,39 @@ __device__ __forceinline__ WyOperands wy_operands(const float* Xb, const float* 
 }
 
 // D[n][t] = sum_j X[j][n] A'[t][j] for this wave's 16 tokens, stored to w / u:
-// the [k | v] tile xs (`pitch` bytes per row, rows in the nat_row order) gives
-// the X^T fragments by ds_read_b64_tr_b16 in the natural order; each lane
-// ends with features 16 nb + 4 grp .. + 3 of token t = 16 wv + li, one 8-byte
-// store.  The products are recompute_w_u's.
+// the [k | v] tile xs (`pitch` bytes per row, rows in the nat_row order)
+// gives the X^T fragments by ds_read_b64_tr_b16 in the natural order; each
+// lane ends with features 16 nb + 4 grp .. + 3 of token t = 16 wv + li.  The
+// products are recompute_w_u's.  Column blocks are taken in pairs
+// (2 m, 2 m + 1) and stored as 16-byte pieces of 8 consecutive features
+// (vmem.h acc_pair_to_b128): 8-byte stores of 4 features put 32-byte runs of
+// 16 rows in one store instruction, which the memory path takes far more
+// slowly.
 template <int K, int V>
 __device__ __forceinline__ void wy_products(const char* xs, int pitch, const WyOperands& op, bf16* w, bf16* u,
                                             int64_t trow) {
   const int lane = lane_id(), grp = lane >> 4;
+  static_assert(K % 32 == 0 && V % 32 == 0, "column pairs do not straddle w and u");
 #pragma unroll
-  for (int nb = 0; nb < (K + V) / 16; ++nb) {
-    const bool is_w = 16 * nb < K;
-    f32x4 acc = zero4();
+  for (int m = 0; m < (K + V) / 32; ++m) {
+    const bool is_w = 32 * m < K;
+    f32x4 acc[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const bf16x8 xh =
-          concat(ds_read_tr16(reinterpret_cast<const bf16*>(xs + hl::ntr_frag_off(32 * s, 0, 16 * nb, lane, pitch))),
-                 ds_read_tr16(reinterpret_cast<const bf16*>(xs + hl::ntr_frag_off(32 * s, 1, 16 * nb, lane, pitch))));
-      acc = mfma16x16x32(xh, is_w ? op.awh[s] : op.auh[s], acc);
-      acc = mfma16x16x32(xh, is_w ? op.awl[s] : op.aul[s], acc);
+    for (int p = 0; p < 2; ++p) {
+      const int nb = 2 * m + p;
+      acc[p] = zero4();
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const bf16x8 xh =
+            concat(ds_read_tr16(reinterpret_cast<const bf16*>(xs + hl::ntr_frag_off(32 * s, 0, 16 * nb, lane, pitch))),
+                   ds_read_tr16(reinterpret_cast<const bf16*>(xs + hl::ntr_frag_off(32 * s, 1, 16 * nb, lane, pitch))));
+        acc[p] = mfma16x16x32(xh, is_w ? op.awh[s] : op.auh[s], acc[p]);
+        acc[p] = mfma16x16x32(xh, is_w ? op.awl[s] : op.aul[s], acc[p]);
+      }
     }
-    const int n = 16 * nb + 4 * grp;
-    if (is_w) store4(w + trow * K + n, acc);
-    else store4(u + trow * V + (n - K), acc);
+    const u32x4 piece = acc_pair_to_b128(acc[0], acc[1]);
+    if (is_w) *reinterpret_cast<u32x4*>(w + trow * K + 32 * m + pair_col(grp)) = piece;
+    else *reinterpret_cast<u32x4*>(u + trow * V + 32 * m - K + pair_col(grp)) = piece;
   }
 }
 
@@ -333,7 +345,7 @@ extern "C" int thm_wy_fwd(const void* k, const void* v, const void* beta, const 
   if (B == 0 || T == 0) return THM_OK;  // empty: nothing is read or written
   if (!k || !v || !beta || !w || !u) return THM_ERR_NULL_POINTER;
   if (((uintptr_t)k % 16) || ((uintptr_t)v % 16)) return THM_ERR_MISALIGNED;
-  if (((uintptr_t)w % 8) || ((uintptr_t)u % 8)) return THM_ERR_MISALIGNED;
+  if (((uintptr_t)w % 16) || ((uintptr_t)u % 16)) return THM_ERR_MISALIGNED;
   if (((uintptr_t)beta % 4) || (g && ((uintptr_t)g % 4))) return THM_ERR_MISALIGNED;
   if (B * (T / kBT) > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
   if (!launch_fits(B * (T / kBT) * H, kWyThreads)) return THM_ERR_BAD_SHAPE;
