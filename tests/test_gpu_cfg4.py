@@ -1,7 +1,8 @@
 """Parity at BASELINE.json's config 4, full size (the bench workload).
 
-The oracle cannot run the whole of config 4 in seconds, so the full-size
-GPU results are checked three ways:
+The full-size GPU results are checked four ways:
+  * every output tensor of recompute_w_u, chunk_fwd_h and chunk_fwd_o against
+    the CPU oracle in float32, one batch row at a time;
   * sampled slices against the CPU oracle (float64): whole sequences of
     sampled (batch, head) pairs for the state recurrence and the full chain
     (against the token-level gated delta rule), sampled chunks for
@@ -87,6 +88,42 @@ def test_cfg4_chunk_fwd_o_sampled_chunks(chain):
         hc = d["h"][b:b + 1, c:c + 1, hh:hh + 1]
         eo = odn.chunk_fwd_o_diff(*(np_(_tile(d[n], b, c, hh)) for n in ("q", "k", "vn", "g")), np_(hc), d["scale"])
         assert_close(_tile(d["o"], b, c, hh), eo, 1e-2, 1e-2, f"o tile {(b, c, hh)}")
+
+
+# Whole tensors at full size, one batch row at a time against the oracle in
+# float32 (a few seconds per row on the host); each kernel is fed the GPU's own
+# upstream outputs.
+def _f32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def test_cfg4_recompute_w_u_full(chain):
+    d = chain
+    for b in range(B):
+        print(f"[cfg4] recompute_w_u full, batch row {b}", flush=True)
+        ew, eu = odn.recompute_w_u_ref(*(_f32(d[n][b:b + 1]) for n in ("k", "v", "beta", "A", "g")),
+                                       dtype=np.float32)
+        assert_close(d["w"][b:b + 1], ew, 1e-2, 1e-2, f"w, batch row {b}")
+        assert_close(d["u"][b:b + 1], eu, 1e-2, 1e-2, f"u, batch row {b}")
+
+
+def test_cfg4_chunk_fwd_h_full(chain):
+    d = chain
+    for b in range(B):
+        print(f"[cfg4] chunk_fwd_h full, batch row {b}", flush=True)
+        eh, evn, eht = odn.chunk_fwd_h_delta(*(_f32(d[n][b:b + 1]) for n in ("k", "w", "u", "g")), dtype=np.float32)
+        assert_close(d["h"][b:b + 1], eh, 1e-2, 1e-2, f"h, batch row {b}")
+        assert_close(d["vn"][b:b + 1], evn, 1e-2, 1e-2, f"v_new, batch row {b}")
+        assert_close(d["ht"][b:b + 1], eht, 1e-2, 1e-2, f"final state, batch row {b}")
+
+
+def test_cfg4_chunk_fwd_o_full(chain):
+    d = chain
+    for b in range(B):
+        print(f"[cfg4] chunk_fwd_o full, batch row {b}", flush=True)
+        eo = odn.chunk_fwd_o_diff(*(_f32(d[n][b:b + 1]) for n in ("q", "k", "vn", "g", "h")), d["scale"],
+                                  dtype=np.float32)
+        assert_close(d["o"][b:b + 1], eo, 1e-2, 1e-2, f"o, batch row {b}")
 
 
 def test_cfg4_chain_matches_token_recurrence(chain):
