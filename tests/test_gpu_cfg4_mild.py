@@ -12,7 +12,9 @@ sequences of 8192 tokens are checked against the float64 oracle:
   * o and the final state of both paths against the token-level gated delta
     rule;
 and each check first shows, on the CPU, that the same oracle with the carry
-dropped lies outside the tolerance.  Tolerance rtol = atol = 1e-2.
+dropped lies outside the tolerance.  Every output tensor of chunk_fwd_h and
+chunk_fwd_o is also checked whole, one batch row at a time, against the
+oracle in float32.  Tolerance rtol = atol = 1e-2.
 """
 from __future__ import annotations
 
@@ -85,3 +87,21 @@ def test_cfg4_mild_chain_matches_token_recurrence(mild):
         for what, o, ht in (("four kernels", d["o"], d["ht"]), ("fused", d["o_fused"], d["ht_fused"])):
             assert_close(o[b:b + 1, :, hh:hh + 1], eo, TOL, TOL, f"{what} o (b={b}, head={hh})")
             assert_close(ht[b:b + 1, hh:hh + 1], eS, TOL, TOL, f"{what} final state (b={b}, head={hh})")
+
+
+def test_cfg4_mild_full_tensors(mild):
+    # Every (batch, head) sequence with the carry visible: chunk_fwd_h's h,
+    # v_new and final state against the delta-form recurrence fed the GPU's
+    # own w, u, and chunk_fwd_o's o against the oracle fed the GPU's h, v_new,
+    # one batch row at a time in float32.
+    d = mild
+    f32 = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    for b in range(B):
+        print(f"[cfg4-mild] full tensors, batch row {b}", flush=True)
+        eh, evn, eht = odn.chunk_fwd_h_delta(*(f32(d[n][b:b + 1]) for n in ("k", "w", "u", "g")), dtype=np.float32)
+        assert_close(d["h"][b:b + 1], eh, TOL, TOL, f"h, batch row {b}")
+        assert_close(d["vn"][b:b + 1], evn, TOL, TOL, f"v_new, batch row {b}")
+        assert_close(d["ht"][b:b + 1], eht, TOL, TOL, f"final state, batch row {b}")
+        eo = odn.chunk_fwd_o_diff(*(f32(d[n][b:b + 1]) for n in ("q", "k", "vn", "g", "h")), d["scale"],
+                                  dtype=np.float32)
+        assert_close(d["o"][b:b + 1], eo, TOL, TOL, f"o, batch row {b}")
