@@ -11,21 +11,23 @@
 //     readers expect;
 //   * reads: every fragment read lands on the logical elements its contract
 //     names (for ds_read_b64_tr_b16 after the instruction's lane transpose),
-//     stays inside the tile and is free of LDS bank conflicts per pass
-//     (64 banks of 4 bytes and 32 lanes per pass for 8-byte reads; 16-byte
-//     reads as measured on gfx950, 32 lanes per pass over 128 banks);
+//     stays inside the tile and is free of LDS bank conflicts under the
+//     measured gfx950 model of lds_banks.h;
 //   * stores: h, v_new and o tiles are covered exactly once, aligned;
 //   * global bounds: every DMA source and store of the extreme
-//     (batch, head, chunk) lies inside its tensor, and the per-lane offsets fit
-//     in 32 bits; the workgroup -> (b * H + head, V-tile) map is a bijection;
+//     (batch, head, chunk) lies inside its tensor, in both pipelines, and the
+//     per-lane offsets fit in 32 bits; the workgroup -> (b * H + head,
+//     V-tile) map is a bijection;
 //   * wait counts: replaying each wave's issue order, the vmcnt the kernel
 //     waits for at the top of chunk c retires exactly the DMA of chunk c (in
 //     the fused kernel, whose w / u DMA runs ahead of its k / q DMA, each
 //     slot is also loaded only after its previous chunk's last read);
-//   * recompute_w_u's [k | v] tile and chunk_fwd_o's v, h and k tiles
-//     (padded, register-staged): the fragments hold the elements the products
-//     need and are read conflict-free; staging stores are bounded in
-//     conflicts;
+//   * recompute_w_u's [k | v] tiles of one or two heads, their staging and
+//     the output staging of w and u (every byte written and read once, the
+//     reads returning what the global stores need), and chunk_fwd_o's v, h
+//     and k tiles (padded, register-staged): the fragments hold the elements
+//     the products need and are read conflict-free; staging stores are
+//     conflict-free or bounded in conflicts;
 //   * the fused WY kernel's [k | v] tile (nat_row order): staging, transposed
 //     reads and form_L's row reads, all conflict-free;
 //   * chunk_fwd_o's pipelined kernel: its walk (desc_walk_at) maps walk
@@ -47,6 +49,7 @@
 #include <vector>
 
 #include "h_layout.h"
+#include "lds_banks.h"
 #include "handout.h"
 #include "pipe_cfg.h"
 
@@ -111,35 +114,11 @@ static void check_tile_dma(int rb, int waves, int n, int64_t ts, const char* wha
 
 enum ReadKind { kTr16, kPair, kRow8 };
 
-// Bank-conflict check of one instruction: `addr[lane]`, `bytes` per lane.
-// 16-byte accesses, as measured on gfx950: passes of 32 lanes over 128 banks of
-// 4 bytes (512 bytes).  Returns the worst bank multiplicity of the two passes.
-// (Under a 16-lane / 64-bank model a 16-byte row pad reads 16 rows without
-// conflicts; on the GPU chunk_fwd_o's k reads at that pad measured 0.11
-// conflict cycles per LDS access, and at a 32-byte pad or in lane order none.)
-static int ways16(const uint32_t* addr) {
-  int worst = 0;
-  for (int p = 0; p < 2; ++p) {
-    int cnt[128] = {0};
-    for (int l = 32 * p; l < 32 * p + 32; ++l)
-      for (int d = 0; d < 4; ++d) worst = std::max(worst, ++cnt[(addr[l] / 4 + d) % 128]);
-  }
-  return worst;
-}
-
-static void check_banks(const uint32_t* addr, int bytes, const char* what, int r0, int c0, int max16 = 1) {
-  if (bytes == 16) {
-    const int w = ways16(addr);
-    CHECK(w <= max16, "%s (r0 %d, c0 %d): 16-byte access is %d-way conflicted", what, r0, c0, w);
-    return;
-  }
-  const int per_pass = 256 / bytes;
-  for (int p = 0; p < 64 / per_pass; ++p) {
-    std::set<uint32_t> banks;
-    for (int l = p * per_pass; l < (p + 1) * per_pass; ++l)
-      for (int d = 0; d < bytes / 4; ++d) banks.insert((addr[l] / 4 + d) % 64);
-    CHECK((int)banks.size() == 64, "%s (r0 %d, c0 %d): pass %d hits %zu of 64 banks", what, r0, c0, p, banks.size());
-  }
+static void check_banks(const uint32_t* addr, int bytes, Access acc, const char* what, int r0, int c0,
+                        int max_ways = 1) {
+  const int w = bank_ways(addr, bytes, acc);
+  CHECK(w <= max_ways, "%s (r0 %d, c0 %d): %d-byte %s is %d-way conflicted", what, r0, c0, bytes,
+        acc == kLdsWrite ? "write" : "read", w);
 }
 
 // One fragment read at block (r0, c0) of a [64 x rb] tile.
@@ -185,7 +164,7 @@ static void check_read(ReadKind kind, int r0, int c0, int rb, const char* what) 
       }
     }
   }
-  check_banks(addr, bytes, what, r0, c0);
+  check_banks(addr, bytes, kLdsRead, what, r0, c0);
 }
 
 // Every 16-row block position a kernel uses for this read kind and tile.
@@ -401,9 +380,22 @@ static void check_fused() {
     const int64_t tsk = sh.H * K * 2, tsv = sh.H * V * 2;
     check_tile_dma(C::kRowK, 4, C::kKDma, tsk, what);
     check_tile_dma(C::kRowU, 4, C::kUDma, tsv, what);
+    // Global bounds of the DMA sources (k, w, q; the u V-tile; the gates) for
+    // the extreme (b, head, chunk, V-tile), as the kernel forms them.
     const int64_t NT = sh.T / 64, b = sh.B - 1, hh = sh.H - 1, cc = NT - 1;
-    const int64_t kc0 = ((b * sh.T) * sh.H + hh) * K * 2;
-    const int64_t uc0 = ((b * sh.T) * sh.H + hh) * V * 2 + (V - 64) * 2;
+    const int64_t kc0 = ((b * sh.T) * sh.H + hh) * K * 2, kcs = 64 * tsk;
+    const int64_t uc0 = ((b * sh.T) * sh.H + hh) * V * 2 + (V - 64) * 2, ucs = 64 * tsv;
+    uint32_t kmax = 0, umax = 0;
+    for (int P = 0; P < 64 * C::kRowK / 16; ++P) kmax = std::max(kmax, hl::dma_src_off(P, C::kRowK, tsk));
+    for (int P = 0; P < 64 * C::kRowU / 16; ++P) umax = std::max(umax, hl::dma_src_off(P, C::kRowU, tsv));
+    CHECK(kc0 + cc * kcs + kmax + 16 <= sh.B * sh.T * sh.H * K * 2, "%s: k / w / q DMA past the tensor", what);
+    CHECK(uc0 + cc * ucs + umax + 16 <= sh.B * sh.T * sh.H * V * 2, "%s: u DMA past the tensor", what);
+    if (HAS_G) {
+      const int64_t gc0 = ((b * sh.T) * sh.H + hh) * 4;
+      CHECK(gc0 + cc * 64 * sh.H * 4 + 63 * sh.H * 4 + 4 <= sh.B * sh.T * sh.H * 4, "%s: gate DMA past g", what);
+    }
+    CHECK(kmax + 16 < (UINT64_C(1) << 32) && umax + 16 < (UINT64_C(1) << 32) && 63 * sh.H * 4 < (INT64_C(1) << 32),
+          "%s: DMA lane offsets past 32 bits", what);
     // Stores of o and v_new: [64 tokens x V] per chunk, quad-transposed lanes.
     Cover co(64, V);
     for (int vt = 0; vt < V / 64; ++vt)
@@ -536,7 +528,7 @@ static void check_small() {
             CHECK(i % C::kOutPitch < C::kCols, "%s: %s write in the row pad", what, which);
             addr[lane] = (uint32_t)i * 4;
           }
-          check_banks(addr, 4, what, blk, r);
+          check_banks(addr, 4, kLdsWrite, what, blk, r);
         }
     wr.exactly_once(what);
     Cover rd(rows, C::kCols / 4);
@@ -559,12 +551,10 @@ static std::pair<int, int> xdecode(uint32_t a, int rb) {
   return {r, (((b / 16) ^ (hl::xswz(r, rb) << 1)) * 8) + (b % 16) / 2};
 }
 
-// recompute_w_u's [k | v] tile (64 rows of n = K + V bf16 elements, xtile_off):
-// the layout is a bijection, the staging stores (thread q writes elements
-// [col, col + ve) of row q / (n / ve), a wave's stores in 256-byte passes) are
-// conflict-free for 16-byte (bf16 inputs, ve = 8) and 8-byte (fp32 inputs as
-// bf16 hi / lo, ve = 4) stores, and the natural-order ds_read_b64_tr_b16
-// fragments hold the elements the products need, conflict-free.
+// recompute_w_u's [k | v] tile of one head (64 rows of n = K + V bf16
+// elements, xtile_off): the layout is a bijection and the natural-order
+// ds_read_b64_tr_b16 fragments hold the elements the products need,
+// conflict-free.
 static void check_xtile(int n, const char* what) {
   const int rows = 64, rb = 2 * n;
   std::vector<int> hit(rows * n, 0);
@@ -582,18 +572,6 @@ static void check_xtile(int n, const char* what) {
   int bad = 0;
   for (int x : hit) bad += x != 1;
   CHECK(bad == 0, "%s: %d tile slots not covered exactly once", what, bad);
-  for (int ve : {8, 4}) {
-    const int cpr = n / ve, bytes = 2 * ve;
-    for (int q0 = 0; q0 < rows * cpr; q0 += 64) {
-      uint32_t addr[64];
-      for (int lane = 0; lane < 64; ++lane) {
-        const int q = q0 + lane, j = q / cpr, col = (q % cpr) * ve;
-        addr[lane] = hl::xtile_off(j, col, rb);
-        CHECK(addr[lane] % bytes == 0, "%s: staging store of row %d col %d misaligned", what, j, col);
-      }
-      check_banks(addr, bytes, what, q0, ve);
-    }
-  }
   for (int k0 = 0; k0 < rows; k0 += 32)
     for (int half = 0; half < 2; ++half)
       for (int c0 = 0; c0 < n; c0 += 16) {
@@ -615,8 +593,116 @@ static void check_xtile(int n, const char* what) {
                   "%s: transposed lane %d element %d holds (%d, %d)", what, lane, r, d.first, d.second);
           }
         }
-        check_banks(addr, 8, what, k0 + 4 * half, c0);
+        check_banks(addr, 8, kLdsRead, what, k0 + 4 * half, c0);
       }
+}
+
+// recompute_w_u's staging of the k and v rows of a tile of HP heads (HP = 2
+// for bf16 inputs with an even head count, else 1) into the heads' xtile_off
+// tiles, one tile of `tile` bytes per head.  Thread q (a wave is 64
+// consecutive q) holds 16 bytes of the k (then v) rows: token j = q / (HP m),
+// head c / m, elements [col, col + ve) of that head's k (v) row, with c = q %
+// (HP m) and m = K / ve (V / ve) pieces per head row.  ve = 8: bf16 inputs,
+// one 16-byte store; ve = 4: fp32 inputs, stored as 8-byte bf16 hi and lo
+// pieces, the lo tile 64 rb bytes after the hi one (same bank pattern).
+// Checked: every element of every head's tile is stored once, at the address
+// its fragment reads decode, and every store instruction is conflict-free.
+static void check_xstage(int K, int V, int HP, int ve, const char* what) {
+  const int n = K + V, rb = 2 * n, tile = 64 * rb * (ve == 4 ? 2 : 1);
+  std::vector<int> hit((size_t)HP * 64 * n, 0);
+  for (int part = 0; part < 2; ++part) {
+    const int m = (part ? V : K) / ve, pieces = 64 * HP * m;
+    CHECK(pieces % (256 * HP) == 0, "%s: %d pieces do not split over %d threads", what, pieces, 256 * HP);
+    for (int q0 = 0; q0 < pieces; q0 += 64) {
+      uint32_t addr[64];
+      for (int lane = 0; lane < 64; ++lane) {
+        const int q = q0 + lane, j = q / (HP * m), c = q % (HP * m), hd = c / m;
+        const int col = (part ? K : 0) + (c % m) * ve;
+        const uint32_t off = hl::xtile_off(j, col, rb);
+        addr[lane] = (uint32_t)(hd * tile) + off;
+        CHECK(off % (2 * ve) == 0 && off + 2 * ve <= (uint32_t)(64 * rb), "%s: piece %d at %u misplaced", what, q, off);
+        for (int i = 0; i < ve; ++i) {
+          const auto d = xdecode(off + 2 * i, rb);
+          CHECK(d.first == j && d.second == col + i, "%s: piece %d element %d lands on (%d, %d)", what, q, i, d.first,
+                d.second);
+          hit[((size_t)hd * 64 + j) * n + col + i]++;
+        }
+      }
+      check_banks(addr, 2 * ve, kLdsWrite, what, q0, part);
+    }
+  }
+  int bad = 0;
+  for (int x : hit) bad += x != 1;
+  CHECK(bad == 0, "%s: %d staged elements not stored exactly once", what, bad);
+}
+
+// recompute_w_u's output staging, in the X tiles' space once the products are
+// done (HP (1 + split) 64 2 (K + V) bytes): the w rows of the tile's 64 tokens
+// x HP heads (K eb bytes each, otile_off order), then its u rows (V eb
+// bytes).  The wave of head hs and tokens 16 wv .. + 15 writes acc[nb]
+// (features 16 nb + 4 grp .. + 3 of token 16 wv + li) as one 4 eb-byte
+// piece; then thread q (a wave is 64 consecutive q) reads 16-byte piece c of
+// token j's HP contiguous w (u) rows (otile_chunk, halves swapped back where
+// otile_half_swapped), the piece it stores to global memory.  Checked: every
+// access inside the space, every staged byte written once and read once, each
+// read returns the bytes its global store needs, and every write and read
+// instruction conflict-free.
+static void check_ostage(int K, int V, int HP, int eb, const char* what) {
+  const int wrow = K * eb, urow = V * eb, space = HP * 64 * 2 * (K + V) * (eb == 4 ? 2 : 1);
+  const bool half = eb == 2;
+  CHECK(HP * 64 * (wrow + urow) == space, "%s: staged rows do not fill the X space", what);
+  auto base = [&](int part) { return part ? HP * 64 * wrow : 0; };
+  auto tag = [&](int part, int hd, int t, int byte) { return ((part * HP + hd) * 64 + t) * 1024 + byte; };
+  std::vector<int> owner(space, -1), reads(space, 0);
+  for (int hs = 0; hs < HP; ++hs)
+    for (int wv = 0; wv < 4; ++wv)
+      for (int nb = 0; nb < (K + V) / 16; ++nb) {
+        uint32_t addr[64];
+        for (int lane = 0; lane < 64; ++lane) {
+          const int grp = lane >> 4, li = lane & 15, t = 16 * wv + li, n = 16 * nb + 4 * grp;
+          const int part = 16 * nb < K ? 0 : 1, rb = part ? urow : wrow, byte = (part ? n - K : n) * eb;
+          const uint32_t a = (uint32_t)base(part) + hl::otile_off(t, hs, HP, byte, rb, half);
+          addr[lane] = a;
+          if (a % (4 * eb) || a + 4 * eb > (uint32_t)space) {
+            CHECK(false, "%s: write of token %d feature %d at %u misplaced", what, t, n, a);
+            continue;
+          }
+          for (int b = 0; b < 4 * eb; ++b) {
+            CHECK(owner[a + b] == -1, "%s: staged byte %u written twice", what, a + b);
+            owner[a + b] = tag(part, hs, t, byte + b);
+          }
+        }
+        check_banks(addr, 4 * eb, kLdsWrite, what, 16 * wv, 16 * nb);
+      }
+  int unset = 0;
+  for (int x : owner) unset += x == -1;
+  CHECK(unset == 0, "%s: %d staged bytes never written", what, unset);
+  for (int part = 0; part < 2; ++part) {
+    const int rb = part ? urow : wrow, m = rb / 16, pieces = 64 * HP * m;
+    CHECK(pieces % (256 * HP) == 0, "%s: %d store pieces do not split over %d threads", what, pieces, 256 * HP);
+    for (int q0 = 0; q0 < pieces; q0 += 64) {
+      uint32_t addr[64];
+      for (int lane = 0; lane < 64; ++lane) {
+        const int q = q0 + lane, j = q / (HP * m), c = q % (HP * m), hd = c / m, cb = (c % m) * 16;
+        const uint32_t a = (uint32_t)base(part) + hl::otile_chunk(j, hd, HP, c % m, rb);
+        const int sw = hl::otile_half_swapped(j, half) ? 8 : 0;
+        addr[lane] = a;
+        if (a % 16 || a + 16 > (uint32_t)space) {
+          CHECK(false, "%s: read of piece %d at %u misplaced", what, q, a);
+          continue;
+        }
+        for (int b = 0; b < 16; ++b) {
+          CHECK(owner[a + (b ^ sw)] == tag(part, hd, j, cb + b), "%s: piece %d byte %d reads the wrong value", what, q,
+                b);
+          reads[a + b]++;
+        }
+      }
+      check_banks(addr, 16, kLdsRead, what, q0, part);
+    }
+  }
+  int bad = 0;
+  for (int x : reads) bad += x != 1;
+  CHECK(bad == 0, "%s: %d staged bytes not read exactly once", what, bad);
 }
 
 // Logical (row, element) at byte `a` of a padded tile (rows `pitch` bytes
@@ -662,14 +748,7 @@ static void check_padded(int rows, int n, int pitch, bool nat, std::vector<int> 
         addr[lane] = nat ? hl::ntile_off(j, col, pitch) : hl::ptile_off(j, col, pitch);
         CHECK(addr[lane] % bytes == 0, "%s: staging store of row %d col %d misaligned", what, j, col);
       }
-      // Worst bank multiplicity per pass.
-      const int per_pass = 256 / bytes;
-      for (int p = 0; p < 64 / per_pass; ++p) {
-        int cnt[64] = {0}, ways = 0;
-        for (int l = p * per_pass; l < (p + 1) * per_pass; ++l)
-          for (int d = 0; d < bytes / 4; ++d) ways = std::max(ways, ++cnt[(addr[l] / 4 + d) % 64]);
-        CHECK(ways <= max_ways, "%s: staging pass %d of q0 %d is %d-way conflicted", what, p, q0, ways);
-      }
+      check_banks(addr, bytes, kLdsWrite, what, q0, ve, max_ways);
     }
   }
   for (int k0 = 0; k0 < rows; k0 += 32)
@@ -695,7 +774,7 @@ static void check_padded(int rows, int n, int pitch, bool nat, std::vector<int> 
                   what, lane, r, d.first, d.second);
           }
         }
-        check_banks(addr, 8, what, k0 + 4 * half, c0);
+        check_banks(addr, 8, kLdsRead, what, k0 + 4 * half, c0);
       }
 }
 
@@ -715,7 +794,7 @@ static void check_row_tile(int n, const char* what) {
                 lane, i);
         }
       }
-      check_banks(addr, 16, what, r0, e0);
+      check_banks(addr, 16, kLdsRead, what, r0, e0);
     }
 }
 
@@ -737,7 +816,7 @@ static void check_nat_row_reads(int n, int kcols, const char* what) {
                 lane, i);
         }
       }
-      CHECK(ways16(addr) == 1, "%s: row read at (%d, %d) is %d-way conflicted", what, r0, e0, ways16(addr));
+      check_banks(addr, 16, kLdsRead, what, r0, e0);
     }
 }
 
@@ -991,6 +1070,16 @@ int main() {
       char what[96];
       std::snprintf(what, sizeof what, "recompute_w_u [k | v] tile K=%d V=%d", K, V);
       check_xtile(K + V, what);
+      for (int HP : {1, 2}) {
+        std::snprintf(what, sizeof what, "recompute_w_u bf16 staging K=%d V=%d HP=%d", K, V, HP);
+        check_xstage(K, V, HP, 8, what);
+        std::snprintf(what, sizeof what, "recompute_w_u bf16 output staging K=%d V=%d HP=%d", K, V, HP);
+        check_ostage(K, V, HP, 2, what);
+      }
+      std::snprintf(what, sizeof what, "recompute_w_u fp32 staging K=%d V=%d", K, V);
+      check_xstage(K, V, 1, 4, what);
+      std::snprintf(what, sizeof what, "recompute_w_u fp32 output staging K=%d V=%d", K, V);
+      check_ostage(K, V, 1, 4, what);
       std::snprintf(what, sizeof what, "chunk_fwd_o h tile K=%d V=%d", K, V);
       check_padded(K, V, hl::tr_pitch(2 * V), true, {4}, V == 64 ? 2 : 1, what);
     }

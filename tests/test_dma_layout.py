@@ -148,6 +148,16 @@ MUTATIONS = [
      "chunk_fwd_o: v / k lane offset at half the element stride"),
     ("h_layout.h", "return (int64_t)it * (256 / (V / 4)) * V * 4; }", "return (int64_t)it * (256 / (V / 4)) * V * 2; }",
      "chunk_fwd_o: h load step at half the row stride"),
+    ("h_layout.h", "return half_swz && ((t >> 3) & 1); }", "return false; }",
+     "recompute_w_u output staging: no half swap (8-byte writes 2-way)"),
+    ("h_layout.h", "return half_swz && ((t >> 3) & 1); }", "return half_swz && ((t >> 2) & 1); }",
+     "recompute_w_u output staging: half swap by the wrong token bit"),
+    ("h_layout.h", "return (uint32_t)((t * hp + head) * row_bytes + ((q ^ (t & 7)) << 4));",
+     "return (uint32_t)((head * 64 + t) * row_bytes + ((q ^ (t & 7)) << 4));",
+     "recompute_w_u output staging: head-major rows (16-byte reads 2-way at 128-byte rows)"),
+    ("h_layout.h", "return (uint32_t)((t * hp + head) * row_bytes + ((q ^ (t & 7)) << 4));",
+     "return (uint32_t)((t * hp + head) * row_bytes + ((q ^ (t & 3)) << 4));",
+     "recompute_w_u output staging: chunk swizzle over 4 tokens"),
 ]
 
 

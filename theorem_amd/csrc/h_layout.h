@@ -115,17 +115,27 @@ THM_HD constexpr uint32_t xtr_frag_off(int k0, int half, int c0, int lane, int r
   return xtile_off(k0 + 8 * (lane >> 4) + 4 * half + ((lane & 15) >> 2), c0 + 4 * (lane & 3), row_bytes);
 }
 
-// recompute_w_u's output staging tile: 64 token rows of row_bytes = n eb
-// (128, 256 or 512 bytes: 64 or 128 features, bf16 or fp32), unpadded.  The
-// MFMA result of a lane is 4 consecutive features of one token, written as
-// one 8-byte (bf16) or 16-byte (fp32) piece; a 32-lane pass writes 16 rows
-// at one logical 16-byte chunk.  Logical chunk q of row r sits at q ^ oswz(r),
-// which puts those 16 rows on 16 distinct chunks of the 256-byte bank window
-// (for 128-byte rows, two rows per window: 8 chunk positions x 2 halves).
-// The global stores read whole 16-byte chunks of consecutive rows back.
-THM_HD constexpr int oswz(int r, int row_bytes) { return row_bytes >= 256 ? (r & 15) : ((r >> 1) & 7); }
-THM_HD constexpr uint32_t otile_off(int r, int byte, int row_bytes) {
-  return (uint32_t)(r * row_bytes + ((((byte >> 4) ^ oswz(r, row_bytes))) << 4) + (byte & 15));
+// recompute_w_u's output staging tile: the w (or u) rows of the tile's 64
+// tokens x hp heads in their global order (physical row t hp + head), each
+// row_bytes = n eb (128 to 512 bytes: 64 or 128 features, bf16 or fp32),
+// unpadded.  The MFMA result of a lane is 4 consecutive features of one
+// token, written as one 8-byte (bf16) or 16-byte (fp32) piece.  LDS writes go
+// in passes of 128 bytes over 32 banks (16 lanes of 8 bytes, 8 of 16); a pass
+// holds 16 (8) consecutive tokens of one head at one logical 16-byte chunk
+// and, for 8-byte pieces, one half of it.  Logical chunk q of token t sits at
+// q ^ (t & 7), and with half_swz the two 8-byte halves of the chunk swap for
+// t & 8: the pass then covers 16 distinct 8-byte slots (8 distinct chunks) of
+// a 128-byte window, conflict-free.  The global stores read whole 16-byte
+// chunks of consecutive physical rows (reads go in passes of 16 lanes over
+// 128 banks: one row of 256 or 512 bytes or two of 128, conflict-free) and
+// swap the halves back where otile_half_swapped.
+THM_HD constexpr uint32_t otile_chunk(int t, int head, int hp, int q, int row_bytes) {
+  return (uint32_t)((t * hp + head) * row_bytes + ((q ^ (t & 7)) << 4));
+}
+THM_HD constexpr bool otile_half_swapped(int t, bool half_swz) { return half_swz && ((t >> 3) & 1); }
+THM_HD constexpr uint32_t otile_off(int t, int head, int hp, int byte, int row_bytes, bool half_swz) {
+  return otile_chunk(t, head, hp, byte >> 4, row_bytes) +
+         (uint32_t)((byte & 15) ^ (otile_half_swapped(t, half_swz) ? 8 : 0));
 }
 
 // chunk_fwd_o's register-staged v, h and k tiles are padded instead of
@@ -141,10 +151,11 @@ THM_HD constexpr uint32_t otile_off(int r, int byte, int row_bytes) {
 //     natural-order tiles store logical row r at physical row nat_row(r) (bits
 //     2 and 3 of r swapped): each pass then reads 8 consecutive physical rows.
 //   * 16-byte row reads of 16 consecutive rows (chunk_fwd_o's k fragments)
-//     are served 32 lanes at a time over 128 banks (512 bytes), as measured
-//     on gfx950: two column groups of 16 rows per pass, which a pitch of
-//     row_bytes + 32 spreads over distinct banks (a 16-byte pad left 0.11
-//     conflict cycles per access).
+//     are served 16 lanes at a time over 128 banks (512 bytes), as measured
+//     on gfx950: a pitch of row_bytes + 32 puts the 16 rows on distinct
+//     16-byte positions of that window (a 16-byte pad measured 0.11 conflict
+//     cycles per access in chunk_fwd_o; at V = 64 it also makes the
+//     transposed reads of the h and v tiles 2-way).
 THM_HD constexpr int tr_pitch(int row_bytes) { return row_bytes + 32; }
 // The fused WY kernel's [k | v] tile (64 rows of n = K + V bf16): natural-order
 // transposed reads in its products and 16-byte row reads (form_L's k

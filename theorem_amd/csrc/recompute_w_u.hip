@@ -182,43 +182,46 @@ recompute_w_u_kernel(const IT* __restrict__ k, const IT* __restrict__ v,
   // 5. Stage w and u through LDS (the X tiles' space, once every wave is done
   // with them) so that the global stores are whole 16-byte pieces of
   // consecutive token rows, the HP heads of a token contiguous: 64 HP rows of
-  // K (V) features per tile.  Stores of 4 features per lane straight from the
-  // accumulators touch 16 rows per instruction (249 against 226 us for the
-  // same bytes stored contiguously, config 4).
-  char* const ob = reinterpret_cast<char*>(&xs[0][0]);
+  // K (V) features per tile, in global order (h_layout.h otile_off; bf16
+  // pieces with the half swap that keeps the 8-byte writes conflict-free).
+  // Stores of 4 features per lane straight from the accumulators touch 16
+  // rows per instruction (249 against 226 us for the same bytes stored
+  // contiguously, config 4).
+  constexpr bool kHalf = !C::kSplitX;  // 8-byte (bf16) pieces
+  char* const owb = reinterpret_cast<char*>(&xs[0][0]);  // w rows
   constexpr int kWRow = K * (int)sizeof(IT), kURow = V * (int)sizeof(IT);
-  char* const owb = ob + hs * kBT * kWRow;                 // this wave's head: w rows
-  char* const oub = ob + HP * kBT * kWRow + hs * kBT * kURow;  // u rows
+  char* const oub = owb + HP * kBT * kWRow;  // u rows
   lds_barrier();  // every wave is done reading X
   const int t = 16 * wv + li;
 #pragma unroll
   for (int nb = 0; nb < C::kNB; ++nb) {
     const int n = 16 * nb + 4 * grp;
     if (16 * nb < K) {
-      lds_store4(owb + hl::otile_off(t, n * (int)sizeof(IT), kWRow), acc[nb], (const IT*)nullptr);
+      lds_store4(owb + hl::otile_off(t, hs, HP, n * (int)sizeof(IT), kWRow, kHalf), acc[nb], (const IT*)nullptr);
     } else {
-      lds_store4(oub + hl::otile_off(t, (n - K) * (int)sizeof(IT), kURow), acc[nb], (const IT*)nullptr);
+      lds_store4(oub + hl::otile_off(t, hs, HP, (n - K) * (int)sizeof(IT), kURow, kHalf), acc[nb], (const IT*)nullptr);
     }
   }
   lds_barrier();
+  // Thread q: 16-byte piece c of token j's HP contiguous w (u) rows.
+  auto piece = [&](const char* base, int j, int c, int row) {
+    u32x4 val = *reinterpret_cast<const u32x4*>(base + hl::otile_chunk(j, c / (row / 16), HP, c % (row / 16), row));
+    if (hl::otile_half_swapped(j, kHalf)) val = u32x4{val[2], val[3], val[0], val[1]};
+    return val;
+  };
   constexpr int kWPieces = kBT * HP * kWRow / 16, kUPieces = kBT * HP * kURow / 16;
   static_assert(kWPieces % C::kThreads == 0 && kUPieces % C::kThreads == 0, "store split");
 #pragma unroll
   for (int it = 0; it < kWPieces / C::kThreads; ++it) {
     const int q = tid + it * C::kThreads;
     const int j = q / (HP * kWRow / 16), c = q - j * (HP * kWRow / 16);
-    const int hsub = c / (kWRow / 16), cb = (c - hsub * (kWRow / 16)) * 16;
-    const u32x4 val = *reinterpret_cast<const u32x4*>(ob + hsub * kBT * kWRow + hl::otile_off(j, cb, kWRow));
-    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(w + ((tok0 + j) * H + h0) * K) + c * 16) = val;
+    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(w + ((tok0 + j) * H + h0) * K) + c * 16) = piece(owb, j, c, kWRow);
   }
 #pragma unroll
   for (int it = 0; it < kUPieces / C::kThreads; ++it) {
     const int q = tid + it * C::kThreads;
     const int j = q / (HP * kURow / 16), c = q - j * (HP * kURow / 16);
-    const int hsub = c / (kURow / 16), cb = (c - hsub * (kURow / 16)) * 16;
-    const u32x4 val =
-        *reinterpret_cast<const u32x4*>(ob + HP * kBT * kWRow + hsub * kBT * kURow + hl::otile_off(j, cb, kURow));
-    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(u + ((tok0 + j) * H + h0) * V) + c * 16) = val;
+    *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(u + ((tok0 + j) * H + h0) * V) + c * 16) = piece(oub, j, c, kURow);
   }
 }
 
