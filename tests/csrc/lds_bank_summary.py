@@ -6,8 +6,10 @@ PROBE_STDOUT holds the probe's lines (launch index, pattern, model slowdown);
 COUNTER_CSV is rocprofv3's counter_collection.csv of the same run with
 SQ_LDS_BANK_CONFLICT, SQ_LDS_IDX_ACTIVE and SQ_INSTS_LDS.  Prints a markdown
 table: conflict cycles and active cycles per LDS instruction, and whether the
-model (tests/csrc/lds_banks.h) agrees: it calls a pattern conflict-free
-exactly when the counter shows no conflict cycles.
+model (tests/csrc/lds_banks.h) agrees: "yes" when it calls a pattern
+conflict-free exactly when the counter shows no conflict cycles,
+"conservative" when it reports a conflict the counter does not show, "NO"
+when it misses one (exit status 1).
 """
 import collections
 import csv
@@ -26,16 +28,23 @@ def main(probe_out: str, counters: str) -> int:
         return 1
     print("| pattern | conflict cycles / instr | active cycles / instr | model | agrees |")
     print("|---|---:|---:|---|---|")
-    bad = 0
+    bad = cons = 0
     for (idx, name, ways), c in zip(pats, rows):
         n = c["SQ_INSTS_LDS"]
         conf, act = c["SQ_LDS_BANK_CONFLICT"] / n, c["SQ_LDS_IDX_ACTIVE"] / n
         model = "conflict-free" if ways == "1" else f"{ways}-way"
-        ok = (ways == "1") == (conf == 0)
-        bad += not ok
-        print(f"| {name} | {conf:.2f} | {act:.2f} | {model} | {'yes' if ok else 'NO'} |")
-    print(f"\n{len(pats) - bad} of {len(pats)} patterns agree with the model.")
-    return 0
+        if (ways == "1") == (conf == 0):
+            verdict = "yes"
+        elif conf == 0:
+            verdict = "conservative"  # the model reports a conflict the counter does not show
+            cons += 1
+        else:
+            verdict = "NO"  # a conflict the model misses
+            bad += 1
+        print(f"| {name} | {conf:.2f} | {act:.2f} | {model} | {verdict} |")
+    print(f"\n{len(pats) - bad - cons} of {len(pats)} patterns agree with the model, {cons} conservatively "
+          f"(reported as a conflict, measured free), {bad} missed.")
+    return 1 if bad else 0
 
 
 if __name__ == "__main__":

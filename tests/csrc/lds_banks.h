@@ -9,16 +9,19 @@
 // against SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE measured per instruction on
 // gfx950 (lds_bank_probe.hip: single-instruction kernels over hand-picked lane
 // patterns; and the counts of this build's kernels):
-//   * 8-byte reads (ds_read_b64, ds_read_b64_tr_b16) go in passes of 32 lanes
-//     over 64 banks of 4 bytes, one cycle each when no bank is hit twice;
+//   * 4-byte reads (ds_read_b32) go in one pass of 64 lanes over 64 banks of
+//     4 bytes, 8-byte reads (ds_read_b64, ds_read_b64_tr_b16) in passes of 32
+//     lanes, one cycle each when no bank is hit twice;
 //   * 16-byte reads (ds_read_b128) go in passes of 32 lanes taking two
 //     cycles at best.  No single bank model fits every measurement: 16-lane
 //     runs of 256 bytes 512 bytes apart read conflict-free (which 128 banks
 //     would make 2-way), while 16 rows 272 bytes apart at two adjacent 16-byte
 //     columns are 2-way (which 64 banks hit at most twice per pass would make
 //     conflict-free).  The check asks for both: each 32-lane pass hits each of
-//     64 banks at most twice and each of 128 banks at most once, which every
-//     pattern measured conflict-free here does;
+//     64 banks at most twice and each of 128 banks at most once.  That holds
+//     for every pattern measured conflict-free here but one (16-lane runs of
+//     256 bytes 512 bytes apart), so it errs only towards reporting a
+//     conflict;
 //   * writes go in passes of 128 bytes over 32 banks (16 lanes of 8 bytes,
 //     8 lanes of 16, 32 lanes of 4), one cycle each when no bank is hit twice
 //     (16 rows 256 bytes apart, one 8-byte piece each at 16 distinct 16-byte
@@ -38,6 +41,6 @@ inline int pass_ways(const uint32_t* addr, int bytes, int per_pass, int banks, i
 inline int bank_ways(const uint32_t* addr, int bytes, Access acc) {
   if (acc == kLdsWrite) return pass_ways(addr, bytes, 128 / bytes, 32, 1);
   if (bytes == 16) return std::max(pass_ways(addr, 16, 32, 64, 2), pass_ways(addr, 16, 32, 128, 1));
-  return pass_ways(addr, bytes, 32, 64, 1);
+  return pass_ways(addr, bytes, bytes == 4 ? 64 : 32, 64, 1);
 }
 
