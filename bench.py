@@ -428,6 +428,7 @@ def pattern_floors(torch, inp, conv_in, reps: int = 5):
         "chunk_fwd_o": (N * (3 * 256 + 4) + NC * 65536, N * 256),
         "wy_fwd": (N * (2 * 256 + 8), N * 2 * 256),
         "chunk_gated_delta_fwd": (N * (4 * 256 + 4), N * 256),
+        "chunk_gated_delta_fwd_a": (N * (4 * 256 + 8), N * 256),
     }
     src = torch.empty(max(r for r, _ in mix.values()), dtype=torch.uint8, device=k.device)
     dst = torch.empty(max(w for _, w in mix.values()), dtype=torch.uint8, device=k.device)
@@ -462,6 +463,11 @@ def pattern_floors(torch, inp, conv_in, reps: int = 5):
         if t is not None:
             out[name]["ceiling_us"] = round(t, 2)
             out[name]["ceiling_GBps"] = round((rd + wr) / t / 1e3, 1)
+    for name in mix.keys() - runs.keys():  # a ceiling only (the A form shares the w / u form's floor)
+        rd, wr = mix[name]
+        t = best_of(lambda: lib.thm_floor_mix(P(src), i64(rd), P(dst), i64(wr), stream))
+        if t is not None:
+            out[name] = {"ceiling_us": round(t, 2), "ceiling_GBps": round((rd + wr) / t / 1e3, 1)}
     del src, dst
     return out
 
@@ -551,11 +557,21 @@ def extension_timings(torch, inp, conv_in, iters: int = 10, settle_s: float = 0.
         lambda: chain.chunk_fwd_fused(inp["q"], inp["k"], ww, uu, inp["g"], inp["scale"], None, True),
         N * (3 * K * 2 + V * 2 + 4) + N * V * 2 + B * H * K * V * 4,
         f"({B},{T},{H},{K},{V}) bf16: chunk_fwd_h + chunk_fwd_o fused, final state out")
+    cases["chunk_gated_delta_fwd_a"] = (
+        lambda: chain.chunk_fwd_fused_a(inp["q"], inp["k"], inp["v"], inp["beta"], inp["A"], inp["g"], inp["scale"],
+                                        None, True),
+        N * (2 * K * 2 + V * 2 + 64 * 4 + 8) + N * V * 2 + B * H * K * V * 4,
+        f"({B},{T},{H},{K},{V}) bf16: recompute_w_u + chunk_fwd_h + chunk_fwd_o fused from A, final state out")
     cases["chunk_gated_delta_rule_fwd"] = (
         lambda: chain.chunk_gated_delta_rule_fwd(inp["q"], inp["k"], inp["v"], inp["beta"], inp["g"], inp["scale"],
                                                  output_final_state=True),
+        N * (K * 2 + 8) + N * 64 * 4 + N * (2 * K * 2 + V * 2 + 64 * 4 + 8) + N * V * 2 + B * H * K * V * 4,
+        "the whole chunked forward from (q, k, v, beta, g): A-builder, then the fused forward from A")
+    cases["chunk_gated_delta_rule_fwd_wy"] = (
+        lambda: chain.chunk_gated_delta_rule_fwd(inp["q"], inp["k"], inp["v"], inp["beta"], inp["g"], inp["scale"],
+                                                 output_final_state=True, fused_form="wy"),
         N * (K * 2 + V * 2 + 8) + N * (K * 2 + V * 2) + N * (3 * K * 2 + V * 2 + 4) + N * V * 2 + B * H * K * V * 4,
-        "the whole chunked forward from (q, k, v, beta, g): fused WY (A, w, u), fused h + o")
+        "the same through w and u: fused WY (A, w, u), fused h + o")
     # The reference's own dtype (fp32; kernel.py asserts it) at config-4 sizes.
     from theorem_amd.kernels import chunk_fwd_h, chunk_fwd_o
     k32, v32, q32 = inp["k"].float(), inp["v"].float(), inp["q"].float()
@@ -692,7 +708,7 @@ def main() -> int:
     ap.add_argument("--no-ext", action="store_true", help="skip the extension kernels (A-builder, gate cumsum, ...)")
     ap.add_argument("--small", action="store_true", help="1/8-size workload (quick check)")
     ap.add_argument("--only", choices=["causal_conv1d", "recompute_w_u", "chunk_fwd_h", "chunk_fwd_o", "wy_build_A",
-                                        "chunk_gated_delta_fwd", "wy_fwd"],
+                                        "chunk_gated_delta_fwd", "chunk_gated_delta_fwd_a", "wy_fwd"],
                     help="run only this kernel of the step (for per-kernel rocprofv3 counter runs)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run a plain 1 GiB device-to-device copy (rocprofv3 counter calibration)")
@@ -796,6 +812,7 @@ def main() -> int:
             "chunk_fwd_o": lambda: chunk_fwd_o.custom_kernel(dict(q=q, k=k, v=vn, g=g, h=h, scale=scale)),
             "wy_build_A": lambda: recompute_w_u.build_A(k, beta, g, sign=+1),
             "chunk_gated_delta_fwd": lambda: chain.chunk_fwd_fused(q, k, w, u, g, scale, None, True),
+            "chunk_gated_delta_fwd_a": lambda: chain.chunk_fwd_fused_a(q, k, v, beta, A, g, scale, None, True),
             "wy_fwd": lambda: chain.wy_fwd(k, v, beta, g, sign=+1),
         }[args.only]
         for _ in range(args.warmup + args.steps):
@@ -873,13 +890,18 @@ def main() -> int:
     if not args.no_ext and not args.small:
         print("[bench] extension kernels", file=sys.stderr, flush=True)
         ext = extension_timings(torch, inp, conv_in)
-        for n in ("wy_fwd", "chunk_gated_delta_fwd"):
-            if floors and n in floors and n in ext:
-                ext[n]["floor_us"] = floors[n]["us"]
-                ext[n]["of_floor"] = round(floors[n]["us"] / ext[n]["us"], 3)
-                if "ceiling_us" in floors[n]:
-                    ext[n]["ceiling_us"] = floors[n]["ceiling_us"]
-                    ext[n]["of_ceiling"] = round(floors[n]["ceiling_us"] / ext[n]["us"], 3)
+        # The A form's floor is the w / u form's pattern floor (the same tiles:
+        # A rows are 256 bytes like w's at K = 128; its 4 more bytes of beta
+        # per token-head are 0.3 % of the bytes); its ceiling is its own mix.
+        for n, fn in (("wy_fwd", "wy_fwd"), ("chunk_gated_delta_fwd", "chunk_gated_delta_fwd"),
+                      ("chunk_gated_delta_fwd_a", "chunk_gated_delta_fwd")):
+            if floors and fn in floors and n in ext:
+                ext[n]["floor_us"] = floors[fn]["us"]
+                ext[n]["of_floor"] = round(floors[fn]["us"] / ext[n]["us"], 3)
+                ceil = floors.get(n, {}).get("ceiling_us", floors[fn].get("ceiling_us"))
+                if ceil is not None:
+                    ext[n]["ceiling_us"] = ceil
+                    ext[n]["of_ceiling"] = round(ceil / ext[n]["us"], 3)
 
     cpu = None
     if not args.no_cpu:

@@ -193,6 +193,27 @@ int thm_chunk_gated_delta_fwd(const void* q, const void* k, const void* w, const
                               int32_t chunk_size, int32_t qkv_dtype, void* stream);
 
 /*
+ * The same recurrence and output from the WY matrix instead of w and u: per
+ * chunk c,
+ *   v_new = A_c (beta_c * (v_c - exp(g_c) * (k_c S)))
+ * which equals u_c - w_c S for w_c = A_c (k_c beta_c exp(g_c)), u_c =
+ * A_c (v_c beta_c) (recompute_w_u, kernels/recompute_w_u/reference.py:118-149),
+ * so w and u are never formed; o, v_new and ht as thm_chunk_gated_delta_fwd.
+ * A is thm_wy_build_A's output (sign = +1 for the gated delta rule).
+ * Replaces recompute_w_u, chunk_fwd_h (delta form) and chunk_fwd_o in the
+ * chunked forward (kernels/recompute_w_u/kernel.py:192-248,
+ * kernels/chunk_fwd_h/kernel.py:141-191, kernels/chunk_fwd_o/kernel.py:146-212);
+ * no single reference function does this.
+ *   bf16 only: q, k, v, o, v_new bf16; beta [B, T, H], A [B, T, H, 64], g, h0,
+ *   ht fp32.  g, h0, v_new, ht may be NULL.  K, V in {64, 128}; T % 64 == 0.
+ *   q, k, v and A 16-byte aligned, o and v_new 8-byte, beta, g, h0, ht 4-byte.
+ */
+int thm_chunk_gated_delta_fwd_a(const void* q, const void* k, const void* v, const void* beta,
+                                const void* A, const void* g, const void* h0, void* o, void* v_new,
+                                void* ht, float scale, int64_t B, int64_t T, int64_t H, int64_t K,
+                                int64_t V, int32_t chunk_size, int32_t qkv_dtype, void* stream);
+
+/*
  * WY matrix of the chunked Gated DeltaNet forward, per chunk c of
  * chunk_size = 64 tokens:
  *   M[i][j] = beta_i (k_i . k_j) exp(g_i - g_j) for j < i (0 on and above the diagonal),

@@ -342,24 +342,31 @@ static void check_h() {
 
 // --------------------------------------------------------------------------- fused
 
-template <int K, int V, bool HAS_G, bool SV>
+template <int K, int V, bool HAS_G, bool SV, bool FROM_A = false>
 static void check_fused() {
-  using C = pipe::FCfg<K, HAS_G, SV>;
+  using C = pipe::FCfg<K, HAS_G, SV, FROM_A>;
   char what[128];
-  std::snprintf(what, sizeof what, "fused K=%d V=%d g=%d vn=%d", K, V, HAS_G, SV);
+  std::snprintf(what, sizeof what, "fused K=%d V=%d g=%d vn=%d A-form=%d", K, V, HAS_G, SV, FROM_A);
   constexpr int KB2 = C::KB / 2;
   {
     std::vector<std::pair<int, int>> reg;
     for (int s = 0; s < pipe::kFStages; ++s) {
       const int base = s * C::kStage;
-      for (int m = 0; m < 3; ++m) reg.push_back({base + m * C::kTileK, base + (m + 1) * C::kTileK});
-      reg.push_back({base + 3 * C::kTileK, base + 3 * C::kTileK + C::kTileU});
-      if (HAS_G) {
-        // gates (DMA), then e^{g_i} and e^{g_last - g_j} (written by state wave 0)
-        const int gb = base + 3 * C::kTileK + C::kTileU;
-        for (int part = 0; part < 3; ++part) reg.push_back({gb + 256 * part, gb + 256 * (part + 1)});
-        CHECK(3 * 256 <= C::kGBytes, "%s: gate block", what);
+      // k, w (A), q, u (v), as the kernel's stage_* place them.
+      reg.push_back({base, base + C::kTileK});
+      reg.push_back({base + C::kTileK, base + C::kTileK + C::kTileW});
+      reg.push_back({base + C::kTileK + C::kTileW, base + 2 * C::kTileK + C::kTileW});
+      const int ub = base + 2 * C::kTileK + C::kTileW;
+      reg.push_back({ub, ub + C::kTileU});
+      if (C::kGates) {
+        // gates (DMA), e^{g_i} and e^{g_last - g_j} (written by state wave 0),
+        // beta (DMA, A form)
+        const int gb = ub + C::kTileU;
+        for (int part = 0; part < 4; ++part)
+          if ((part < 3 && HAS_G) || (part == 3 && FROM_A)) reg.push_back({gb + 256 * part, gb + 256 * (part + 1)});
+        CHECK(4 * 256 <= C::kGBytes, "%s: gate block", what);
       }
+      CHECK(ub + C::kTileU + (C::kGates ? C::kGBytes : 0) == base + C::kStage, "%s: stage %d size", what, s);
     }
     const int lp = pipe::kFStages * C::kStage;
     reg.push_back({lp, lp + C::kPBytes});
@@ -374,6 +381,48 @@ static void check_fused() {
     // Hand-over slots: S pairs (wq, s2 < KB2) and v_new pairs (wq, s2 < 2), 16 bytes per lane.
     CHECK(((3 * KB2 + KB2 - 1) * 64 + 63) * 16 + 16 <= C::kSBytes, "%s: S hand-over slots", what);
     CHECK(((3 * 2 + 1) * 64 + 63) * 16 + 16 <= C::kVBytes, "%s: v_new hand-over slots", what);
+  }
+  if (FROM_A) {
+    // P1's A fragments: row block ib, pair s2, lane (li, grp) reads fp32
+    // elements 32 s2 + 4 grp .. + 3 and 32 s2 + 16 + 4 grp .. + 3 of row
+    // 16 ib + li as two 16-byte reads of the DMA'd A tile (tile_off of the
+    // element pair index), conflict-free.
+    for (int ib = 0; ib < 4; ++ib)
+      for (int s2 = 0; s2 < 2; ++s2)
+        for (int half = 0; half < 2; ++half) {
+          uint32_t addr[64];
+          for (int lane = 0; lane < 64; ++lane) {
+            const int row = 16 * ib + (lane & 15), j0 = 32 * s2 + 16 * half + 4 * (lane >> 4);
+            addr[lane] = hl::tile_off(row, 2 * j0, C::kRowW);
+            CHECK(addr[lane] % 16 == 0 && addr[lane] + 16 <= (uint32_t)C::kTileW, "%s: A fragment at %u", what, addr[lane]);
+            for (int e = 0; e < 8; ++e) {
+              const auto d = decode(addr[lane] + 2 * e, C::kRowW);
+              CHECK(d.first == row && d.second == 2 * j0 + e, "%s: A fragment lane %d element %d holds (%d, %d)", what,
+                    lane, e, d.first, d.second);
+            }
+          }
+          check_banks(addr, 16, kLdsRead, what, 16 * ib, 32 * s2 + 16 * half);
+        }
+    // prepare(): state wave wq converts, in place, the 16-byte pieces of its
+    // quarter of the A tile, bytes [wq kTileW / 4, (wq + 1) kTileW / 4):
+    // exactly the pieces its own DMA wrote (slots (wq kWDma + i) 64 + lane),
+    // so it needs no other wave's DMA; the quarters tile the A tile.
+    std::vector<int> conv(C::kTileW / 16, 0);
+    for (int wq = 0; wq < 4; ++wq) {
+      std::set<int> dma, mine;
+      for (int i = 0; i < C::kWDma; ++i)
+        for (int lane = 0; lane < 64; ++lane) dma.insert((wq * C::kWDma + i) * 64 + lane);
+      for (int i = 0; i < C::kTileW / 4 / 16 / 64; ++i)
+        for (int lane = 0; lane < 64; ++lane) {
+          const int piece = (wq * (C::kTileW / 4) + 16 * (lane + 64 * i)) / 16;
+          mine.insert(piece);
+          conv[piece]++;
+        }
+      CHECK(dma == mine, "%s: state wave %d converts pieces its DMA did not write", what, wq);
+    }
+    int badc = 0;
+    for (int x : conv) badc += x != 1;
+    CHECK(badc == 0, "%s: %d A pieces not converted exactly once", what, badc);
   }
   for (const Shape& sh : kShapes) {
     if (64 * sh.H * (K > V ? K : V) * 2 > (INT64_C(1) << 31)) continue;
@@ -396,6 +445,19 @@ static void check_fused() {
     }
     CHECK(kmax + 16 < (UINT64_C(1) << 32) && umax + 16 < (UINT64_C(1) << 32) && 63 * sh.H * 4 < (INT64_C(1) << 32),
           "%s: DMA lane offsets past 32 bits", what);
+    if (FROM_A) {
+      // A rows (64 fp32 per token-head, 256 bytes for any K) and the beta gather.
+      const int64_t tsa = sh.H * 256;
+      if (64 * tsa <= (INT64_C(1) << 31)) {
+        check_tile_dma(C::kRowW, 4, C::kWDma, tsa, what);
+        uint32_t amax = 0;
+        for (int P = 0; P < 64 * C::kRowW / 16; ++P) amax = std::max(amax, hl::dma_src_off(P, C::kRowW, tsa));
+        const int64_t ac0 = ((b * sh.T) * sh.H + hh) * 256;
+        CHECK(ac0 + cc * 64 * tsa + amax + 16 <= sh.B * sh.T * sh.H * 256, "%s: A DMA past the tensor", what);
+      }
+      const int64_t bc0 = ((b * sh.T) * sh.H + hh) * 4;
+      CHECK(bc0 + cc * 64 * sh.H * 4 + 63 * sh.H * 4 + 4 <= sh.B * sh.T * sh.H * 4, "%s: beta DMA past beta", what);
+    }
     // Stores of o and v_new: [64 tokens x V] per chunk, quad-transposed lanes.
     Cover co(64, V);
     for (int vt = 0; vt < V / 64; ++vt)
@@ -426,7 +488,7 @@ static void check_fused() {
   for (int NT = 1; NT <= 5; ++NT)
     for (int wq = 0; wq < 4; ++wq) {
       WaveOps w;
-      const int nkq = 2 * C::kKDma + ((HAS_G && wq == 0) ? 1 : 0);
+      const int nkq = 2 * C::kKDma + ((HAS_G && wq == 0) ? 1 : 0) + ((FROM_A && wq == 1) ? 1 : 0);
       w.dma(0, C::kWuDma);
       w.dma(0, nkq);
       for (int x = 1; x < C::kWuLead; ++x) w.dma(x < NT ? x : -2, C::kWuDma);
@@ -1060,7 +1122,11 @@ int main() {
   check_fused<K, V, true, true>();    \
   check_fused<K, V, true, false>();   \
   check_fused<K, V, false, true>();   \
-  check_fused<K, V, false, false>();
+  check_fused<K, V, false, false>();  \
+  check_fused<K, V, true, true, true>();   \
+  check_fused<K, V, true, false, true>();  \
+  check_fused<K, V, false, true, true>();  \
+  check_fused<K, V, false, false, true>();
   F_ALL(64, 64)
   F_ALL(64, 128)
   F_ALL(128, 64)

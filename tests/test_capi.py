@@ -26,6 +26,7 @@ def test_header_lists_entry_points():
     syms = declared_symbols()
     assert {"thm_causal_conv1d_fwd", "thm_recompute_w_u_fwd", "thm_chunk_fwd_h",
             "thm_chunk_fwd_o", "thm_wy_build_A", "thm_chunk_local_cumsum", "thm_wy_fwd",
+            "thm_chunk_gated_delta_fwd", "thm_chunk_gated_delta_fwd_a",
             "thm_status_string", "thm_abi_version"} <= set(syms)
 
 
@@ -158,6 +159,24 @@ def test_build_A_and_cumsum_validation():
     assert wy(K=96) == -4 and wy(V=32) == -4 and wy(bt=32) == -6 and wy(sign=2) == -6
     assert wy(k=FAKE + 8) == -5 and wy(v=FAKE + 8) == -5 and wy(w=FAKE + 4) == -5 and wy(g=FAKE + 2) == -5
     assert wy(B=0) == 0 and wy(T=0) == 0
+
+    def fa(**kw):
+        a = dict(q=FAKE, k=FAKE, v=FAKE, beta=FAKE, A=FAKE, g=FAKE, h0=None, o=FAKE, vn=None, ht=None, B=1, T=64,
+                 H=2, K=64, V=128, bt=64, qd=1)
+        a.update(kw)
+        return lib.thm_chunk_gated_delta_fwd_a(a["q"], a["k"], a["v"], a["beta"], a["A"], a["g"], a["h0"], a["o"],
+                                               a["vn"], a["ht"], ctypes.c_float(1.0), a["B"], a["T"], a["H"],
+                                               a["K"], a["V"], a["bt"], a["qd"], None)
+
+    assert fa(q=None) == -1 and fa(k=None) == -1 and fa(v=None) == -1 and fa(beta=None) == -1
+    assert fa(A=None) == -1 and fa(o=None) == -1
+    assert fa(T=65) == -2 and fa(H=0) == -2 and fa(B=-1) == -2
+    assert fa(qd=0) == -3 and fa(K=96) == -4 and fa(V=32) == -4 and fa(bt=32) == -6
+    assert fa(A=FAKE + 8) == -5 and fa(v=FAKE + 8) == -5 and fa(beta=FAKE + 2) == -5 and fa(o=FAKE + 4) == -5
+    assert fa(B=0) == 0 and fa(T=0) == 0
+    # A rows are 256 bytes for any K: the 32-bit lane-offset guard binds at
+    # 64 H 256 > 2^31 also for K = V = 64.
+    assert fa(K=64, V=64, H=(1 << 17) + 1) == -4
 
     def cs(**kw):
         a = dict(a=FAKE, g=FAKE, B=1, T=64, H=2, bt=64, ad=0, mode=0)

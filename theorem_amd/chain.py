@@ -4,8 +4,9 @@
     (w, u) = recompute_w_u(k, v, beta, A, g)                            HIP
     (h, v_new, S) = chunk_fwd_h delta form (h[c] before chunk c)        HIP
     o      = chunk_fwd_o(q, k, v_new, g, h, scale)                      HIP
-    (for bf16 the first two fused into one kernel, wy_fwd, and the last
-    two into another, chunk_fwd_fused)
+    (for bf16 the last three in one kernel from A, chunk_fwd_fused_a, which
+    never forms w and u; or the first two in one kernel, wy_fwd, and the last
+    two in another, chunk_fwd_fused)
 
 The reference never composes its ops (each is tested alone); this is the
 forward of chunked Gated DeltaNet that the three ops are the stages of, and
@@ -93,16 +94,47 @@ def chunk_fwd_fused(q, k, w, u, g, scale: float, initial_state=None, output_fina
     return o, vn, ht
 
 
+def chunk_fwd_fused_a(q, k, v, beta, A, g, scale: float, initial_state=None, output_final_state: bool = False,
+                      save_new_value: bool = False):
+    """The same as chunk_fwd_fused from the WY matrix A instead of w and u:
+    v_new = A (beta (v - e^g k S)) = u - w S per chunk, in one HIP kernel
+    (thm_chunk_gated_delta_fwd_a; bf16 q, k, v; fp32 beta, A, g).  Returns
+    (o, v_new or None, ht or None)."""
+    B, T, H, K = k.shape
+    V = v.shape[-1]
+    assert T % BT == 0, f"T={T} must be a multiple of {BT}"
+    assert q.shape == k.shape and v.shape[:3] == (B, T, H) and beta.shape == (B, T, H)
+    assert A.shape == (B, T, H, BT) and (g is None or g.shape == (B, T, H))
+    assert q.dtype == k.dtype == v.dtype == torch.bfloat16, "the fused path is bf16-only"
+    _capi.require_device(q, k, v, beta, A, g, initial_state)
+    for name, t in (("beta", beta), ("A", A), ("g", g), ("initial_state", initial_state)):
+        _capi.require_f32(t, name)
+    q, k, v, beta, A, g, h0 = (_capi.prep(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta"),
+                                                             (A, "A"), (g, "g"), (initial_state, "initial_state")))
+    o = torch.empty_like(v)
+    vn = torch.empty_like(v) if save_new_value else None
+    ht = torch.empty(B, H, K, V, dtype=torch.float32, device=k.device) if output_final_state else None
+    status = _capi.load_library().thm_chunk_gated_delta_fwd_a(
+        _capi.ptr(q), _capi.ptr(k), _capi.ptr(v), _capi.ptr(beta), _capi.ptr(A), _capi.ptr(g), _capi.ptr(h0),
+        _capi.ptr(o), _capi.ptr(vn), _capi.ptr(ht), float(scale), B, T, H, K, V, BT,
+        _capi.THM_DTYPE[torch.bfloat16], _capi.stream_of(k))
+    _capi.check(status, "thm_chunk_gated_delta_fwd_a")
+    return o, vn, ht
+
+
 def chunk_gated_delta_rule_fwd(q, k, v, beta, g, scale: float, initial_state=None,
                                output_final_state: bool = False, A: torch.Tensor | None = None,
                                return_intermediates: bool = False, a: torch.Tensor | None = None,
-                               a_logsigmoid: bool = False, fused: bool | None = None):
+                               a_logsigmoid: bool = False, fused: bool | None = None,
+                               fused_form: str = "A"):
     """o [B, T, H, V] (dtype of q) and the final state [B, H, K, V] fp32 (or None).
 
-    bf16 inputs run two fused kernels (``fused``, default for bf16 unless
-    ``return_intermediates``, which needs A and the per-chunk states h): wy_fwd
-    (A and w, u; unless ``A`` is given) and chunk_fwd_fused (the state
-    recurrence and the output); otherwise build_A, recompute_w_u, chunk_fwd_h,
+    bf16 inputs run fused kernels (``fused``, default for bf16 unless
+    ``return_intermediates``, which needs w, u and the per-chunk states h):
+    with ``fused_form`` "A" (default) build_A (unless ``A`` is given) and
+    chunk_fwd_fused_a (w and u never formed: recurrence and output from A);
+    with "wy" wy_fwd (A and w, u in one kernel; unless ``A`` is given) and
+    chunk_fwd_fused.  Otherwise build_A, recompute_w_u, chunk_fwd_h,
     chunk_fwd_o.
     ``g`` is the chunk-local cumulative log decay [B, T, H] fp32 (or None: no
     gate).  Alternatively pass the per-token log decay ``a`` (g = None): g is
@@ -115,6 +147,12 @@ def chunk_gated_delta_rule_fwd(q, k, v, beta, g, scale: float, initial_state=Non
         g = chunk_local_cumsum(a, logsigmoid=a_logsigmoid)
     if fused is None:
         fused = k.dtype == torch.bfloat16 and not return_intermediates
+    assert fused_form in ("A", "wy"), fused_form
+    if fused and fused_form == "A":
+        if A is None:
+            A = build_A(k, beta, g)
+        o, _, ht = chunk_fwd_fused_a(q, k, v, beta, A, g, scale, initial_state, output_final_state)
+        return o, ht
     if fused and A is None:
         w, u = wy_fwd(k, v, beta, g, sign=+1)
     else:

@@ -12,6 +12,17 @@
 // state before chunk c; nothing of either reference kernel's output but o
 // (and optionally v_new and the final state) is written.
 //
+// The A form (FROM_A, thm_chunk_gated_delta_fwd_a) takes the chunk's WY
+// matrix A, v and beta instead of w and u:
+//   v_new = A (beta (v - e^{g} k S))
+// equals u - w S for the recompute_w_u outputs u = A (v beta), w =
+// A (k beta e^g) (kernels/recompute_w_u/reference.py:118-149), so the chunked
+// forward needs neither w nor u in HBM: A (64 fp32 per token-head) replaces
+// w (K bf16) in the w slot and v replaces u in the u slot.  P1 forms
+// k S as the w form forms w S, t = beta (v - e^g k S) as bf16 B-operand
+// pairs, then A t with A as bf16 hi + lo operands (converted in place once
+// per chunk, see prepare below).
+//
 // Structure: one 512-thread workgroup per (b, head, V-tile), 8 wavefronts in
 // two roles that share SIMDs pairwise; wave role and column group wq (columns
 // 16 wq .. 16 wq + 15 of the tile) are wave-uniform:
@@ -38,7 +49,8 @@
 // wait at the top of the loop is an exact count of the ops they issue after
 // the chunk's k / q DMA (pipe_cfg.h FCfg); the output waves issue stores only.
 // HBM traffic per token-head: k, w and q (K eb each), u (V eb) and g (4 B)
-// read once; o (V eb) written once (+ v_new when requested).  The V-tiles of
+// read once; o (V eb) written once (+ v_new when requested).  The A form
+// reads A (256 B) in place of w and beta (4 B) besides.  The V-tiles of
 // one (b, head) run on one XCD, so their second read of k, w, q is meant to
 // hit that XCD's L2.
 #include "h_layout.h"
@@ -55,14 +67,16 @@ using pipe::kFStages;
 using pipe::kFThreads;
 constexpr int kFBV = pipe::kTileV;  // V-tile width
 
-template <int K, int V, bool HAS_G, bool STORE_VN>
+template <int K, int V, bool HAS_G, bool STORE_VN, bool FROM_A>
 __global__ void __launch_bounds__(kFThreads)
 chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
                        const bf16* __restrict__ w, const bf16* __restrict__ u,
+                       const float* __restrict__ A, const float* __restrict__ beta,
                        const float* __restrict__ g, const float* __restrict__ h0,
                        bf16* __restrict__ o, bf16* __restrict__ vnew, float* __restrict__ ht,
                        float scale, int64_t T, int64_t H, int64_t NT, int64_t BH) {
-  using C = FCfg<K, HAS_G, STORE_VN>;
+  // FROM_A: w = nullptr, u = v (the u slot holds v), A and beta given.
+  using C = FCfg<K, HAS_G, STORE_VN, FROM_A>;
   constexpr int NVT = V / kFBV;
   constexpr int KB2 = C::KB / 2;
   __shared__ __attribute__((aligned(1024))) char lds[C::kLds];
@@ -79,11 +93,11 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   const int lane = tid & 63, grp = lane >> 4, li = lane & 15;
 
   auto stage_k = [&](int s) { return lds + s * C::kStage; };
-  auto stage_w = [&](int s) { return lds + s * C::kStage + C::kTileK; };
-  auto stage_q = [&](int s) { return lds + s * C::kStage + 2 * C::kTileK; };
-  auto stage_u = [&](int s) { return lds + s * C::kStage + 3 * C::kTileK; };
+  auto stage_w = [&](int s) { return lds + s * C::kStage + C::kTileK; };  // w, or A (FROM_A)
+  auto stage_q = [&](int s) { return lds + s * C::kStage + C::kTileK + C::kTileW; };
+  auto stage_u = [&](int s) { return lds + s * C::kStage + 2 * C::kTileK + C::kTileW; };  // u, or v
   auto stage_g = [&](int s) {
-    return reinterpret_cast<float*>(lds + s * C::kStage + 3 * C::kTileK + C::kTileU);
+    return reinterpret_cast<float*>(lds + s * C::kStage + 2 * C::kTileK + C::kTileW + C::kTileU);
   };
   char* const lp = lds + kFStages * C::kStage;  // P[i][j], 128-byte rows, swizzled
   // Hand-over slots, lane-major: 16 bytes per lane per B-operand pair.
@@ -96,8 +110,10 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   const int64_t uc0 = ((b * T) * H + hh) * V * 2 + v0 * 2;
   const int64_t gc0 = ((b * T) * H + hh) * 4;
   const int64_t kcs = kBT * tsk, ucs = kBT * tsv, gcs = kBT * H * 4;
+  // A rows (FROM_A): 64 fp32 per token-head.
+  const int64_t tsa = H * kBT * 4, ac0 = ((b * T) * H + hh) * kBT * 4, acs = kBT * tsa;
 
-  uint32_t koff[C::kKDma], uoff[C::kUDma];
+  uint32_t koff[C::kKDma], uoff[C::kUDma], aoff[FROM_A ? C::kWDma : 1];
 #pragma unroll
   for (int i = 0; i < C::kKDma; ++i) {
     const int P = (wq * C::kKDma + i) * 64 + lane;
@@ -107,6 +123,13 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   for (int i = 0; i < C::kUDma; ++i) {
     const int P = (wq * C::kUDma + i) * 64 + lane;
     uoff[i] = hl::dma_src_off(P, C::kRowU, tsv);
+  }
+  if constexpr (FROM_A) {
+#pragma unroll
+    for (int i = 0; i < C::kWDma; ++i) {
+      const int P = (wq * C::kWDma + i) * 64 + lane;
+      aoff[i] = hl::dma_src_off(P, C::kRowW, tsa);
+    }
   }
   const uint32_t goff = (uint32_t)(lane * H * 4);
 
@@ -133,11 +156,24 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
           dma_b32(gb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s))));
         }
       }
+      if constexpr (FROM_A) {
+        if (wq == 1) {  // beta, after the gate factors
+          const char* bb = reinterpret_cast<const char*>(beta) + gc0 + cc * gcs;
+          dma_b32(bb, goff, __builtin_amdgcn_readfirstlane(lds_address(stage_g(s) + 192)));
+        }
+      }
     }
   };
-  // DMA of chunk cc's w and u tiles into stage s.
+  // DMA of chunk cc's w and u (A and v) tiles into stage s.
   auto issue_wu = [&](int64_t cc, int s) {
-    issue_tile(w, cc, stage_w(s));
+    if constexpr (FROM_A) {
+      const char* ab = reinterpret_cast<const char*>(A) + ac0 + cc * acs;
+      const uint32_t la = lds_address(stage_w(s)) + wq * C::kWDma * 1024;
+#pragma unroll
+      for (int i = 0; i < C::kWDma; ++i) dma_b128(ab, aoff[i], __builtin_amdgcn_readfirstlane(la + i * 1024));
+    } else {
+      issue_tile(w, cc, stage_w(s));
+    }
     const char* ub = reinterpret_cast<const char*>(u) + uc0 + cc * ucs;
     const uint32_t lu = lds_address(stage_u(s)) + wq * C::kUDma * 1024;
 #pragma unroll
@@ -181,39 +217,62 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       S[kb][r] = (state_wave && h0) ? h0[st_base + (int64_t)(16 * kb + 4 * grp + r) * V + ncol] : 0.f;
   wait_vmcnt<0>();  // retire the h0 loads before the counted loop
 
+  // Once a chunk's tiles are in LDS (this wave has waited for its own DMA of
+  // them), before the barrier that opens the chunk (state waves):
+  //   * the chunk's gate factors, once per workgroup (state wave 0, one token
+  //     per lane), into the stage's gate block after the gates (which the DMA
+  //     fills, bytes 0-255): e^{g_i} at +64 floats (the output's global term
+  //     and, in the A form, P1), e^{g_last - g_j} at +128 (the state update);
+  //   * A form: each state wave turns the 16 rows of A it loaded (4 KiB of
+  //     the tile) into bf16 hi / lo in place, each 16-byte piece of 4 fp32
+  //     becoming 4 hi then 4 lo, so P1 reads MFMA operands directly.
+  // Both happen at the end of the chunk before, where the state waves wait
+  // for the output waves anyway, rather than at the top of P1.
+  auto prepare = [&](int sp) {
+    if constexpr (HAS_G) {
+      if (wq == 0) {
+        float* const ge = stage_g(sp);
+        const float gt = ge[lane];
+        ge[64 + lane] = fast_exp(gt);
+        ge[128 + lane] = fast_exp(ge[kBT - 1] - gt);
+      }
+    }
+    if constexpr (FROM_A) {
+      char* const ta = stage_w(sp) + wq * (C::kTileW / 4);
+#pragma unroll
+      for (int i = 0; i < C::kTileW / 4 / 16 / 64; ++i) {
+        u32x4* const pc = reinterpret_cast<u32x4*>(ta + 16 * (lane + 64 * i));
+        const f32x4 x = __builtin_bit_cast(f32x4, *pc);
+        bf16x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          hi[e] = (bf16)x[e];
+          lo[e] = (bf16)(x[e] - (float)hi[e]);
+        }
+        const u32x2 h2 = __builtin_bit_cast(u32x2, hi), l2 = __builtin_bit_cast(u32x2, lo);
+        *pc = u32x4{h2[0], h2[1], l2[0], l2[1]};
+      }
+    }
+  };
+
   if (state_wave && NT > 0) {
     issue_wu(0, 0);
 #pragma unroll
     for (int m = 0; m < 3; ++m) issue_part(0, 0, m);
 #pragma unroll
     for (int x = 1; x < C::kWuLead; ++x) issue_wu(x < NT ? x : NT - 1, x % kFStages);
+    wait_vmcnt<C::kWaitFirst>();  // chunk 0's tiles are in
+    prepare(0);
   }
   for (int64_t c = 0; c < NT; ++c) {
     const int s = (int)(c % kFStages);
-    if (state_wave) {
-      if (c < kFStages - 1) wait_vmcnt<C::kWaitFirst>();
-      else wait_vmcnt<C::kWaitSteady>();
-    }
-    lds_barrier();  // A: chunk c is in LDS; every wave is done with chunk c - 1
+    lds_barrier();  // A: chunk c is in LDS and prepared; every wave is done with chunk c - 1
     const char* tk = stage_k(s);
     const char* tq = stage_q(s);
-    const float* gs = HAS_G ? stage_g(s) : nullptr;
+    const float* gs = C::kGates ? stage_g(s) : nullptr;
 
     f32x4 vn[4];    // state waves: v_new rows j = 16 jb + 4 grp + r of column 16 wq + li
     bf16x8 vp[2];   // state waves: v_new as bf16 B-operand pairs
-    if constexpr (HAS_G) {
-      // The chunk's gate factors, once per workgroup (state wave 0, one token
-      // per lane), into the stage's gate block after the gates (which the DMA
-      // fills, bytes 0-255): e^{g_i} for the output's global term at +64
-      // floats, e^{g_last - g_j} for the state update at +128.  Read after
-      // barrier M; the next write is after the next barrier A.
-      if (state_wave && wq == 0) {
-        float* const ge = stage_g(s);
-        const float gt = ge[lane];
-        ge[64 + lane] = fast_exp(gt);
-        ge[128 + lane] = fast_exp(ge[kBT - 1] - gt);
-      }
-    }
     if (state_wave) {
       // The next chunk's k / q / g DMA is issued in parts between P1's row
       // blocks, so the address unit drains between parts while the MFMAs run.
@@ -232,13 +291,69 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
       // P1: v_new = u - w S.
       const char* tw = stage_w(s);
       const char* tu = stage_u(s);
+      if constexpr (FROM_A) {
+        // v_new = A t with t_j = beta_j (v_j - e^{g_j} k_j . S) = (v beta - k
+        // beta e^g S)_j: A (v beta) = u, A (k beta e^g) = w.  t as bf16
+        // B-operand pairs; A (fp32) as bf16 hi + lo A operands.
+        f32x4 t4[4];
+        // A fragments of row blocks 0 and 1 read before the products with S
+        // (those of blocks 2 and 3 after them: all of them up front spilled),
+        // so the first products with t do not wait on LDS.
+        u32x4 af[4][2][2];
 #pragma unroll
-      for (int jb = 0; jb < 4; ++jb) {
-        issue_part(cnc, cns, jb);
-        const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(tu + hl::tr_frag_off(16 * jb, 16 * wq, lane, C::kRowU)));
+        for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
-        vn[jb] -= rows_times_S(tw, jb, sb);
+          for (int s2 = 0; s2 < 2; ++s2) {
+            if (2 * s2 > ib) continue;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+              af[ib][s2][hf] = *reinterpret_cast<const u32x4*>(tw + hl::tile_off(16 * ib + li, 2 * (32 * s2 + 16 * hf + 4 * grp), C::kRowW));
+          }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          issue_part(cnc, cns, jb);
+          const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(tu + hl::tr_frag_off(16 * jb, 16 * wq, lane, C::kRowU)));
+          const f32x4 ks = rows_times_S(tk, jb, sb);
+          const f32x4 bt = *reinterpret_cast<const f32x4*>(gs + 192 + 16 * jb + 4 * grp);  // beta_j
+          f32x4 eg = {1.f, 1.f, 1.f, 1.f};
+          if constexpr (HAS_G) eg = *reinterpret_cast<const f32x4*>(gs + 64 + 16 * jb + 4 * grp);  // e^{g_j}
+#pragma unroll
+          for (int r = 0; r < 4; ++r) t4[jb][r] = bt[r] * ((float)t[r] - eg[r] * ks[r]);
+        }
+        bf16x8 tp[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const float f[8] = {t4[2 * s2][0], t4[2 * s2][1], t4[2 * s2][2], t4[2 * s2][3],
+                              t4[2 * s2 + 1][0], t4[2 * s2 + 1][1], t4[2 * s2 + 1][2], t4[2 * s2 + 1][3]};
+          tp[s2] = to_bf16x8(f);
+        }
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+          vn[ib] = zero4();
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            if (2 * s2 > ib) continue;  // A is lower triangular
+            // Each 16-byte piece holds 4 elements as bf16 hi then lo (prepare).
+            if (ib >= 2)
+#pragma unroll
+              for (int hf = 0; hf < 2; ++hf)
+                af[ib][s2][hf] = *reinterpret_cast<const u32x4*>(tw + hl::tile_off(16 * ib + li, 2 * (32 * s2 + 16 * hf + 4 * grp), C::kRowW));
+            const u32x4 x0 = af[ib][s2][0], x1 = af[ib][s2][1];
+            const bf16x8 ah = __builtin_bit_cast(bf16x8, u32x4{x0[0], x0[1], x1[0], x1[1]});
+            const bf16x8 al = __builtin_bit_cast(bf16x8, u32x4{x0[2], x0[3], x1[2], x1[3]});
+            vn[ib] = mfma16x16x32(ah, tp[s2], vn[ib]);
+            vn[ib] = mfma16x16x32(al, tp[s2], vn[ib]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          issue_part(cnc, cns, jb);
+          const bf16x4 t = ds_read_tr16(reinterpret_cast<const bf16*>(tu + hl::tr_frag_off(16 * jb, 16 * wq, lane, C::kRowU)));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vn[jb][r] = (float)t[r];
+          vn[jb] -= rows_times_S(tw, jb, sb);
+        }
       }
       if constexpr (STORE_VN) {
         bf16* vb = vnew + ((b * T + c * kBT) * H + hh) * V;
@@ -340,6 +455,11 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
           S[kb] = mfma16x16x32(concat(a, bq), vh[s2], S[kb]);
         }
       }
+      // Chunk c + 1's tiles (this wave's DMA of them) are in: prepare its stage.
+      if (c + 1 < NT) {
+        wait_vmcnt<C::kWaitSteady>();
+        prepare((int)((c + 1) % kFStages));
+      }
     } else {
       // Output, one 16-row query block at a time: o = scale (e^{g_i} q S + P v_new).
       bf16x8 sb[KB2];
@@ -380,16 +500,17 @@ chunk_fwd_fused_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
   }
 }
 
-template <int K, int V>
-hipError_t launch_fused(const void* q, const void* k, const void* w, const void* u, const void* g,
-                        const void* h0, void* o, void* vnew, void* ht, float scale, int64_t B,
-                        int64_t T, int64_t H, hipStream_t s) {
+template <int K, int V, bool FROM_A>
+hipError_t launch_fused(const void* q, const void* k, const void* w, const void* u, const void* A,
+                        const void* beta, const void* g, const void* h0, void* o, void* vnew, void* ht,
+                        float scale, int64_t B, int64_t T, int64_t H, hipStream_t s) {
   const int64_t NT = T / kBT, BH = B * H;
   const dim3 grid((unsigned)(BH * (V / kFBV)));
-#define THM_FUSED_LAUNCH(HG, SV)                                                                  \
-  hipLaunchKernelGGL((chunk_fwd_fused_kernel<K, V, HG, SV>), grid, dim3(kFThreads), 0, s,         \
-                     (const bf16*)q, (const bf16*)k, (const bf16*)w, (const bf16*)u, (const float*)g, \
-                     (const float*)h0, (bf16*)o, (bf16*)vnew, (float*)ht, scale, T, H, NT, BH)
+#define THM_FUSED_LAUNCH(HG, SV)                                                                   \
+  hipLaunchKernelGGL((chunk_fwd_fused_kernel<K, V, HG, SV, FROM_A>), grid, dim3(kFThreads), 0, s,  \
+                     (const bf16*)q, (const bf16*)k, (const bf16*)w, (const bf16*)u, (const float*)A, \
+                     (const float*)beta, (const float*)g, (const float*)h0, (bf16*)o, (bf16*)vnew,  \
+                     (float*)ht, scale, T, H, NT, BH)
   if (g) {
     if (vnew) THM_FUSED_LAUNCH(true, true);
     else THM_FUSED_LAUNCH(true, false);
@@ -401,6 +522,43 @@ hipError_t launch_fused(const void* q, const void* k, const void* w, const void*
   return hipGetLastError();
 }
 
+// Shared argument checks and dispatch of both entry points (FROM_A: w = A,
+// u = v, beta given).
+template <bool FROM_A>
+int fused_entry(const void* q, const void* k, const void* w, const void* u, const void* beta,
+                const void* g, const void* h0, void* o, void* v_new, void* ht, float scale, int64_t B,
+                int64_t T, int64_t H, int64_t K, int64_t V, int32_t chunk_size, int32_t qkv_dtype,
+                void* stream) {
+  if (chunk_size != kBT) return THM_ERR_BAD_ARGUMENT;
+  if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || T % kBT) return THM_ERR_BAD_SHAPE;
+  if (qkv_dtype != THM_DTYPE_BF16) return THM_ERR_BAD_DTYPE;  // the fused path is bf16-only
+  if ((K != 64 && K != 128) || (V != 64 && V != 128)) return THM_ERR_UNSUPPORTED;
+  if (B == 0) return THM_OK;
+  if (T == 0 && !ht) return THM_OK;
+  if (T > 0 && (!q || !k || !w || !u || !o || (FROM_A && !beta))) return THM_ERR_NULL_POINTER;
+  const void* p16[] = {q, k, w, u};
+  for (const void* p : p16)
+    if (p && ((uintptr_t)p % 16)) return THM_ERR_MISALIGNED;
+  const void* p4[] = {g, h0, ht, beta};
+  for (const void* p : p4)
+    if (p && ((uintptr_t)p % 4)) return THM_ERR_MISALIGNED;
+  if (((uintptr_t)o % 8) || (v_new && ((uintptr_t)v_new % 8))) return THM_ERR_MISALIGNED;
+  if (B > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
+  if (!launch_fits(B * H * (V / kFBV), kFThreads)) return THM_ERR_BAD_SHAPE;
+  // 32-bit lane offsets (A rows are 256 bytes for any K).
+  const int64_t row_max = (K > V ? K : V) * 2 > 256 || !FROM_A ? (K > V ? K : V) * 2 : 256;
+  if (64 * H * row_max > (INT64_C(1) << 31)) return THM_ERR_UNSUPPORTED;
+  hipStream_t s = (hipStream_t)stream;
+  const void* wp = FROM_A ? nullptr : w;
+  const void* ap = FROM_A ? w : nullptr;
+  hipError_t e;
+  if (K == 64 && V == 64) e = launch_fused<64, 64, FROM_A>(q, k, wp, u, ap, beta, g, h0, o, v_new, ht, scale, B, T, H, s);
+  else if (K == 64 && V == 128) e = launch_fused<64, 128, FROM_A>(q, k, wp, u, ap, beta, g, h0, o, v_new, ht, scale, B, T, H, s);
+  else if (K == 128 && V == 64) e = launch_fused<128, 64, FROM_A>(q, k, wp, u, ap, beta, g, h0, o, v_new, ht, scale, B, T, H, s);
+  else e = launch_fused<128, 128, FROM_A>(q, k, wp, u, ap, beta, g, h0, o, v_new, ht, scale, B, T, H, s);
+  return (int)e;
+}
+
 }  // namespace
 }  // namespace thm
 
@@ -409,29 +567,15 @@ extern "C" int thm_chunk_gated_delta_fwd(const void* q, const void* k, const voi
                                          void* ht, float scale, int64_t B, int64_t T, int64_t H,
                                          int64_t K, int64_t V, int32_t chunk_size,
                                          int32_t qkv_dtype, void* stream) {
-  using namespace thm;
-  if (chunk_size != kBT) return THM_ERR_BAD_ARGUMENT;
-  if (B < 0 || T < 0 || H <= 0 || K <= 0 || V <= 0 || T % kBT) return THM_ERR_BAD_SHAPE;
-  if (qkv_dtype != THM_DTYPE_BF16) return THM_ERR_BAD_DTYPE;  // the fused path is bf16-only
-  if ((K != 64 && K != 128) || (V != 64 && V != 128)) return THM_ERR_UNSUPPORTED;
-  if (B == 0) return THM_OK;
-  if (T == 0 && !ht) return THM_OK;
-  if (T > 0 && (!q || !k || !w || !u || !o)) return THM_ERR_NULL_POINTER;
-  const void* p16[] = {q, k, w, u};
-  for (const void* p : p16)
-    if (p && ((uintptr_t)p % 16)) return THM_ERR_MISALIGNED;
-  const void* p4[] = {g, h0, ht};
-  for (const void* p : p4)
-    if (p && ((uintptr_t)p % 4)) return THM_ERR_MISALIGNED;
-  if (((uintptr_t)o % 8) || (v_new && ((uintptr_t)v_new % 8))) return THM_ERR_MISALIGNED;
-  if (B > (INT64_C(1) << 31) / H) return THM_ERR_BAD_SHAPE;
-  if (!launch_fits(B * H * (V / kFBV), kFThreads)) return THM_ERR_BAD_SHAPE;
-  if (64 * H * (K > V ? K : V) * 2 > (INT64_C(1) << 31)) return THM_ERR_UNSUPPORTED;  // 32-bit lane offsets
-  hipStream_t s = (hipStream_t)stream;
-  hipError_t e;
-  if (K == 64 && V == 64) e = launch_fused<64, 64>(q, k, w, u, g, h0, o, v_new, ht, scale, B, T, H, s);
-  else if (K == 64 && V == 128) e = launch_fused<64, 128>(q, k, w, u, g, h0, o, v_new, ht, scale, B, T, H, s);
-  else if (K == 128 && V == 64) e = launch_fused<128, 64>(q, k, w, u, g, h0, o, v_new, ht, scale, B, T, H, s);
-  else e = launch_fused<128, 128>(q, k, w, u, g, h0, o, v_new, ht, scale, B, T, H, s);
-  return (int)e;
+  return thm::fused_entry<false>(q, k, w, u, nullptr, g, h0, o, v_new, ht, scale, B, T, H, K, V, chunk_size,
+                                 qkv_dtype, stream);
+}
+
+extern "C" int thm_chunk_gated_delta_fwd_a(const void* q, const void* k, const void* v, const void* beta,
+                                           const void* A, const void* g, const void* h0, void* o,
+                                           void* v_new, void* ht, float scale, int64_t B, int64_t T,
+                                           int64_t H, int64_t K, int64_t V, int32_t chunk_size,
+                                           int32_t qkv_dtype, void* stream) {
+  return thm::fused_entry<true>(q, k, A, v, beta, g, h0, o, v_new, ht, scale, B, T, H, K, V, chunk_size,
+                                qkv_dtype, stream);
 }

@@ -64,25 +64,34 @@ struct PCfg {
 // stage c % 2 are free from that barrier on, and those tiles get one and a half
 // chunk periods to arrive.  There is no L2 prefetch: beside the early w / u
 // DMA, every prefetch variant measured slower.
+// The A form (FROM_A) reads the chunk's WY matrix A (64 fp32 per row) in the w
+// slot, v in the u slot and beta after the gates: its P1 forms v_new =
+// A (beta (v - e^g k S)), which equals u - w S, so w and u are never formed.
 constexpr int kFThreads = 512;     // 4 state + 4 output wavefronts
 constexpr int kFStages = 2;
 
-template <int K, bool HAS_G, bool STORE_VN>
+template <int K, bool HAS_G, bool STORE_VN, bool FROM_A = false>
 struct FCfg {
-  static constexpr int kRowK = K * 2;             // bytes per k / w / q row
+  static constexpr int kRowK = K * 2;             // bytes per k / q (/ w) row
   static constexpr int kTileK = kBT * kRowK;
-  static constexpr int kRowU = kTileV * 2;        // bytes per u row of the V-tile
+  static constexpr int kRowW = FROM_A ? kBT * 4 : kRowK;  // bytes per w row, or per A row
+  static constexpr int kTileW = kBT * kRowW;
+  static constexpr int kRowU = kTileV * 2;        // bytes per u (v) row of the V-tile
   static constexpr int kTileU = kBT * kRowU;
-  static constexpr int kGBytes = 1024;            // the chunk's 64 gates, padded to 1 KiB
-  static constexpr int kStage = 3 * kTileK + kTileU + (HAS_G ? kGBytes : 0);
+  // The gate block: the chunk's 64 gates (+0), the gate factors e^{g_i}
+  // (+64 floats) and e^{g_last - g_j} (+128), beta in the A form (+192).
+  static constexpr bool kGates = HAS_G || FROM_A;
+  static constexpr int kGBytes = 1024;
+  static constexpr int kStage = 2 * kTileK + kTileW + kTileU + (kGates ? kGBytes : 0);
   static constexpr int KB = K / 16;               // 16-row state tiles per column group
   static constexpr int kPBytes = kBT * kBT * 2;   // the chunk's scores P, bf16
   static constexpr int kSBytes = 4 * (KB / 2) * 64 * 16;  // S handed over as bf16 B-operand pairs
   static constexpr int kVBytes = 4 * 2 * 64 * 16;         // v_new handed over the same way
   static constexpr int kLds = kFStages * kStage + kPBytes + kSBytes + kVBytes;
-  static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per state wave per k / w / q tile
+  static constexpr int kKDma = kTileK / 1024 / 4; // 1 KiB DMA instructions per state wave per k / q tile
+  static constexpr int kWDma = kTileW / 1024 / 4; // ... per w (A) tile
   static constexpr int kUDma = kTileU / 1024 / 4;
-  static constexpr int kWuDma = kKDma + kUDma;    // a chunk's w and u tiles, per state wave
+  static constexpr int kWuDma = kWDma + kUDma;    // a chunk's w and u (A and v) tiles, per state wave
   static constexpr int kStores = STORE_VN ? 4 : 0;  // v_new row tiles per state wave
   // Issue schedule, in chunks of lead: chunk x's k, q and gates are DMA'd in
   // P1 of chunk x - kKqLead, its w and u after the mid-chunk barrier of chunk

@@ -46,6 +46,7 @@ SIGNATURES = {
     "thm_chunk_fwd_o": [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, ctypes.c_float,
                         _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_vp],
     "thm_chunk_gated_delta_fwd": [_c_vp] * 9 + [ctypes.c_float] + [_c_i64] * 5 + [_c_i32, _c_i32, _c_vp],
+    "thm_chunk_gated_delta_fwd_a": [_c_vp] * 10 + [ctypes.c_float] + [_c_i64] * 5 + [_c_i32, _c_i32, _c_vp],
     "thm_wy_build_A": [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
                        _c_i32, _c_i32, _c_i32, _c_vp],
     "thm_chunk_local_cumsum": [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_vp],

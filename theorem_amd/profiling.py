@@ -33,6 +33,7 @@ UNITS = {
     "chunk_fwd_o": "chunk_fwd_o.hip",
     "wy_build_A": "wy_build_A.hip",
     "chunk_gated_delta_fwd": "chunk_fwd_fused.hip",
+    "chunk_gated_delta_fwd_a": "chunk_fwd_fused.hip",
     "wy_fwd": "wy_fwd.hip",
 }
 
