@@ -882,6 +882,36 @@ static void check_nat_row_reads(int n, int kcols, const char* what) {
     }
 }
 
+// The WY inversion's 16x16 fp32 blocks (wy_blocks.h through h_layout.h): the
+// accumulator writes and the A operand reads of block_mm are conflict-free,
+// its B operand reads at most 2-way, and each access lands on the element
+// its role names, inside the block's rows.
+static void check_wy_blocks() {
+  const char* what = "WY inversion blocks";
+  for (int r = 0; r < 4; ++r) {
+    uint32_t addr[64];
+    for (int lane = 0; lane < 64; ++lane) {
+      const int o = hl::wy_put_off(lane, r);
+      CHECK(o / hl::kWyPitch == 4 * (lane >> 4) + r && o % hl::kWyPitch == (lane & 15), "%s: put lane %d", what, lane);
+      addr[lane] = 4 * o;
+    }
+    check_banks(addr, 4, kLdsWrite, what, r, 0);
+  }
+  for (int q = 0; q < 4; ++q) {
+    uint32_t pa[64], qa[64];
+    for (int lane = 0; lane < 64; ++lane) {
+      const int a = hl::wy_a_off(lane, q), b = hl::wy_b_off(lane, q);
+      CHECK(a / hl::kWyPitch == (lane & 15) && a % hl::kWyPitch == 4 * q + (lane >> 4), "%s: A operand lane %d", what, lane);
+      CHECK(b / hl::kWyPitch == 4 * q + (lane >> 4) && b % hl::kWyPitch == (lane & 15), "%s: B operand lane %d", what, lane);
+      pa[lane] = 4 * a;
+      qa[lane] = 4 * b;
+    }
+    check_banks(pa, 4, kLdsRead, what, q, 0);
+    check_banks(qa, 4, kLdsRead, what, q, 1, 2);
+  }
+  CHECK(hl::kWyPitch >= 16, "%s: pitch below the block's width", what);
+}
+
 // The XCD-aware tile order of recompute_w_u and the A-builder: a bijection of
 // [0, BNT H); when BNT is a multiple of 8 the H heads of one (b, chunk) get
 // launch indices of one residue mod 8 (one XCD).
@@ -1085,6 +1115,7 @@ static void check_o_offsets() {
 }
 
 int main() {
+  check_wy_blocks();
   // Read patterns of both kernels: k / w / q rows (128 or 256 bytes), the u
   // V-tile (128 bytes) and the fused kernel's score tile P (128 bytes).
   for (int rb : {128, 256}) {

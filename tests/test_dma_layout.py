@@ -150,6 +150,10 @@ MUTATIONS = [
      "chunk_fwd_o: h load step at half the row stride"),
     ("h_layout.h", "return half_swz && ((t >> 3) & 1); }", "return false; }",
      "recompute_w_u output staging: no half swap (8-byte writes 2-way)"),
+    ("h_layout.h", "constexpr int kWyPitch = 20;", "constexpr int kWyPitch = 17;",
+     "WY blocks: pitch 17 (2-way accumulator writes)"),
+    ("h_layout.h", "constexpr int kWyPitch = 20;", "constexpr int kWyPitch = 16;",
+     "WY blocks: pitch 16 (4-way A operand reads)"),
     ("h_layout.h", "return half_swz && ((t >> 3) & 1); }", "return half_swz && ((t >> 2) & 1); }",
      "recompute_w_u output staging: half swap by the wrong token bit"),
     ("h_layout.h", "return (uint32_t)((t * hp + head) * row_bytes + ((q ^ (t & 7)) << 4));",

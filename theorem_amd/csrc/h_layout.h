@@ -115,6 +115,21 @@ THM_HD constexpr uint32_t xtr_frag_off(int k0, int half, int c0, int lane, int r
   return xtile_off(k0 + 8 * (lane >> 4) + 4 * half + ((lane & 15) >> 2), c0 + 4 * (lane & 3), row_bytes);
 }
 
+// The WY inversion's 16x16 fp32 blocks in LDS (wy_blocks.h), rows kWyPitch
+// floats apart.  Under gfx950's LDS bank model (4-byte writes in 32-lane
+// passes over 32 banks, 4-byte reads in one 64-lane pass over 64 banks) a
+// pitch of 20 makes the accumulator writes (block_put, form_L) and the A
+// operand reads of block_mm conflict-free and leaves its B operand reads
+// 2-way; no pitch serves all three (17 left all three 2-way: A-builder
+// 110.8 -> 105.5 us at config 4, fused WY 233.2 -> 231.4, bit-identical).
+// Float offsets within a block, lane (g = lane / 16, l = lane % 16):
+//   accumulator row 4 g + r, column l;  A operand row l, column 4 q + g;
+//   B operand row 4 q + g, column l.
+constexpr int kWyPitch = 20;
+THM_HD constexpr int wy_put_off(int lane, int r) { return (4 * (lane >> 4) + r) * kWyPitch + (lane & 15); }
+THM_HD constexpr int wy_a_off(int lane, int q) { return (lane & 15) * kWyPitch + 4 * q + (lane >> 4); }
+THM_HD constexpr int wy_b_off(int lane, int q) { return (4 * q + (lane >> 4)) * kWyPitch + (lane & 15); }
+
 // recompute_w_u's output staging tile: the w (or u) rows of the tile's 64
 // tokens x hp heads in their global order (physical row t hp + head), each
 // row_bytes = n eb (128 to 512 bytes: 64 or 128 features, bf16 or fp32),

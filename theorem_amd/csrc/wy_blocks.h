@@ -12,13 +12,14 @@
 // solve_triangular for the inverse).
 #pragma once
 
+#include "h_layout.h"
 #include "mfma.h"
 
 namespace thm {
 namespace wy {
 
 constexpr int kBT = 64;
-constexpr int kBP = 17;         // LDS pitch (floats) of a 16x16 block
+constexpr int kBP = hl::kWyPitch;  // LDS pitch (floats) of a 16x16 block (h_layout.h)
 constexpr int kBlk = 16 * kBP;  // floats per block
 constexpr int kLdsFloats = 10 * kBlk + 10 * kBlk + 3 * kBlk;  // L, X, per-level T
 
@@ -32,16 +33,16 @@ __device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
 // acc += P Q for 16x16 blocks P, Q in LDS (pitch kBP): lane (g, l) feeds
 // P[l][4q + g] and Q[4q + g][l] at k-step q; acc[r] = row 4g + r, column l.
 __device__ __forceinline__ f32x4 block_mm(const float* P, const float* Q, f32x4 acc) {
-  const int lane = lane_id(), g = lane >> 4, l = lane & 15;
+  const int lane = lane_id();
 #pragma unroll
-  for (int q = 0; q < 4; ++q) acc = mfma16x16x4f32(P[l * kBP + 4 * q + g], Q[(4 * q + g) * kBP + l], acc);
+  for (int q = 0; q < 4; ++q) acc = mfma16x16x4f32(P[hl::wy_a_off(lane, q)], Q[hl::wy_b_off(lane, q)], acc);
   return acc;
 }
 
 __device__ __forceinline__ void block_put(float* D, f32x4 acc, float sgn) {
-  const int lane = lane_id(), g = lane >> 4, l = lane & 15;
+  const int lane = lane_id();
 #pragma unroll
-  for (int r = 0; r < 4; ++r) D[(4 * g + r) * kBP + l] = sgn * acc[r];
+  for (int r = 0; r < 4; ++r) D[hl::wy_put_off(lane, r)] = sgn * acc[r];
 }
 
 // L blocks of one chunk from k fragments fh[tb][s] = k[16 tb + li][32 s + 8 grp .. + 7]
@@ -70,7 +71,7 @@ __device__ __forceinline__ void form_L(const bf16x8 (&fh)[4][KS], const bf16x8 (
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 16 * ib + 4 * grp + r;
-      Lb[p * kBlk + (4 * grp + r) * kBP + li] =
+      Lb[p * kBlk + hl::wy_put_off(lane, r)] =
           (j < i) ? (float)SIGN * sb[i] * acc[r] * fast_exp(sg[i] - sg[j]) : 0.f;
     }
   }
