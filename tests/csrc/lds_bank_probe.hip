@@ -120,12 +120,33 @@ std::vector<Pattern> patterns() {
       [](int l) { return hl::otile_chunk(l / 32, (l / 16) % 2, 2, l % 16, 256); });
   add(ps, "ds_read_b64_tr_b16 recompute_w_u [k | v] fragments", kTr,
       [](int l) { return hl::xtr_frag_off(0, 0, 16, l, 512); });
+  // The DMA pipelines' swizzled chunk tiles (h_layout.h tile_off): 256-byte
+  // k / w / q rows and the fused kernel's 128-byte score rows.
+  for (int e0 : {0, 32})
+    add(ps, "ds_read_b128 row fragments, 256-B swizzled rows, e0 " + std::to_string(e0), kR16,
+        [&](int l) { return hl::row8_frag_off(16, e0, l, 256); });
+  for (int e0 : {0, 16})
+    add(ps, "ds_read_b64 paired fragments, 256-B swizzled rows, e0 " + std::to_string(e0), kR8,
+        [&](int l) { return hl::pair_frag_off(16, e0, l, 256); });
+  add(ps, "ds_read_b64_tr_b16 transposed fragments, 256-B swizzled rows", kTr,
+      [](int l) { return hl::tr_frag_off(32, 16, l, 256); });
+  for (int jb : {0, 1})
+    add(ps, "ds_write_b64 score blocks, 128-B swizzled rows, jb " + std::to_string(jb), kW8,
+        [&](int l) { return hl::pair_frag_off(48, 16 * jb, l, 128); });
+  add(ps, "ds_read_b64 score pairs, 128-B swizzled rows", kR8, [](int l) { return hl::pair_frag_off(48, 32, l, 128); });
+  // 16 rows of 256 bytes, lane (g, r) at chunk (q + g) ^ (r & 14): rows 2m
+  // and 2m + 1 share a chunk.  The model calls this conflict-free and the
+  // hardware serves it 2-way, so the model is a fit to the patterns above,
+  // not the hardware's rule.
+  for (int q : {0, 8})
+    add(ps, "ds_read_b128 16 rows, row pairs at one chunk, q " + std::to_string(q), kR16,
+        [&](int l) { return (uint32_t)(4096 + (l & 15) * 256 + (((q + (l >> 4)) ^ (l & 14)) << 4)); });
   return ps;
 }
 
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
   const std::vector<Pattern> ps = patterns();
   for (const Pattern& p : ps)
     for (int l = 0; l < 64; ++l)
@@ -133,6 +154,23 @@ int main() {
         std::fprintf(stderr, "bad offset: %s lane %d at %u\n", p.name.c_str(), l, p.off[l]);
         return 1;
       }
+  // --model: the model's verdicts only, no GPU (to set beside a stored run).
+  if (argc > 1 && std::string(argv[1]) == "--model") {
+    for (size_t i = 0; i < ps.size(); ++i) {
+      const Access acc = ps[i].op <= kW16 ? kLdsWrite : kLdsRead;
+      std::printf("%zu\t%s\t%d\n", i, ps[i].name.c_str(), bank_ways(ps[i].off.data(), kBytes[ps[i].op], acc));
+    }
+    return 0;
+  }
+  // --addresses: each pattern's 64 lane offsets (to fit other models to a stored run).
+  if (argc > 1 && std::string(argv[1]) == "--addresses") {
+    for (size_t i = 0; i < ps.size(); ++i) {
+      std::printf("%zu\t%s\t%d\t%d", i, ps[i].name.c_str(), kBytes[ps[i].op], ps[i].op <= kW16 ? 1 : 0);
+      for (int l = 0; l < 64; ++l) std::printf("%c%u", l ? ',' : '\t', ps[i].off[l]);
+      std::printf("\n");
+    }
+    return 0;
+  }
   uint32_t *doff = nullptr, *dout = nullptr;
   if (hipMalloc(&doff, 64 * sizeof(uint32_t)) != hipSuccess ||
       hipMalloc(&dout, kGrid * 64 * sizeof(uint32_t)) != hipSuccess) {

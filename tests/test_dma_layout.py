@@ -66,9 +66,6 @@ MUTATIONS = [
     ("h_layout.h", "((((r & 7) ^ ((r >> 3) & 1)) << 1) | ((r >> 3) & 1))",
      "((((r & 7) ^ ((r >> 3) & 1)) << 1) | ((r >> 2) & 1))",
      "swz: wrong row bit (bank conflicts)"),
-    ("h_layout.h", "((((r & 7) ^ ((r >> 3) & 1)) << 1) | ((r >> 3) & 1))",
-     "(((r & 7) << 1) | ((r >> 3) & 1))",
-     "swz: bit 3 not folded into the pair index (conflicted score fragments)"),
     ("h_layout.h", "return tile_off(r0 + 4 * (lane >> 4) + ((lane & 15) >> 2), c0 + 4 * (lane & 3), row_bytes);",
      "return tile_off(r0 + 4 * (lane >> 4) + ((lane & 15) >> 2), c0 + 4 * ((lane + 1) & 3), row_bytes);",
      "tr_frag_off: column group of the neighbouring lane"),

@@ -6,7 +6,7 @@
 // A chunk tile is 64 rows (tokens) of `row_bytes` = 128 or 256 bytes (64 / 128
 // bf16 features), stored in LDS without padding.  The 16-byte chunks of row r
 // are XOR-swizzled: logical chunk q sits at physical chunk q ^ swz(r).  The
-// swizzle makes the three read patterns of the kernels conflict-free:
+// swizzle serves the three read patterns of the kernels:
 //   * 16 consecutive rows (16-aligned), one 16-byte chunk each (w rows as the
 //     A operand, paired order, two 8-byte reads per 256-byte pass): swz takes
 //     16 distinct values over those rows (row_bytes 256), or distinct values
@@ -14,11 +14,11 @@
 //   * 8 consecutive rows (8-aligned), one aligned 32-byte chunk pair each
 //     (ds_read_b64_tr_b16 fragments of k^T and of the u tile): swz >> 1 takes 8
 //     distinct values (row_bytes 256) or 4 per row parity (row_bytes 128);
-//   * 16-byte reads of 16 consecutive rows at two adjacent chunks (the fused
-//     kernel's score fragments), which gfx950 serves 32 lanes over 512 bytes
-//     at a time: swz >> 1 takes 8 distinct values within each row parity
-//     (row_bytes 256), or 4 over each class of rows mod 4 (row_bytes 128).
-//     Hence the XOR of bit 3 into the pair index.
+//   * 16-byte reads of 16 consecutive rows at one chunk per 16-lane pass (the
+//     fused kernel's score fragments and the A form's A fragments): 2-way as
+//     measured on gfx950 (tests/csrc/lds_bank_probe.hip).  Freeing them (a
+//     timing-only lane-order copy of the scores, a row-pair swizzle of the A
+//     tile) did not speed the kernel up.
 // A DMA instruction writes 1 KiB = 64 lanes x 16 bytes at consecutive physical
 // chunks; lane data is fetched from the logical chunk that belongs there.
 #pragma once
@@ -116,12 +116,12 @@ THM_HD constexpr uint32_t xtr_frag_off(int k0, int half, int c0, int lane, int r
 }
 
 // The WY inversion's 16x16 fp32 blocks in LDS (wy_blocks.h), rows kWyPitch
-// floats apart.  Under gfx950's LDS bank model (4-byte writes in 32-lane
-// passes over 32 banks, 4-byte reads in one 64-lane pass over 64 banks) a
-// pitch of 20 makes the accumulator writes (block_put, form_L) and the A
-// operand reads of block_mm conflict-free and leaves its B operand reads
-// 2-way; no pitch serves all three (17 left all three 2-way: A-builder
-// 110.8 -> 105.5 us at config 4, fused WY 233.2 -> 231.4, bit-identical).
+// floats apart.  Under gfx950's LDS bank model (4-byte writes and reads in
+// 32-lane passes over 32 banks) a pitch of 20 makes the accumulator writes
+// (block_put, form_L) conflict-free and leaves block_mm's operand reads
+// 2-way; no pitch makes all three conflict-free (17 left all three 2-way:
+// A-builder 110.8 -> 105.5 us at config 4, fused WY 233.2 -> 231.4,
+// bit-identical).
 // Float offsets within a block, lane (g = lane / 16, l = lane % 16):
 //   accumulator row 4 g + r, column l;  A operand row l, column 4 q + g;
 //   B operand row 4 q + g, column l.
