@@ -11,6 +11,8 @@ the kernel's sources beside them.
 
     python -m theorem_amd.profiling traffic OUT.json CALIB_FETCH_DIR CALIB_WRITE_DIR COPY_BYTES \\
         name=unit:symbol_prefix:algorithmic_bytes:FETCH_DIR:WRITE_DIR ...
+
+``unit`` is a key of ``UNITS`` or the kernel's ``.hip`` file under csrc/.
 """
 from __future__ import annotations
 
@@ -41,6 +43,8 @@ _INC = re.compile(r'^\s*#\s*include\s+"([^"]+)"', re.M)
 
 
 def _sources(unit: str) -> list[Path]:
+    if not (CSRC / unit).is_file():
+        raise FileNotFoundError(f"no kernel source {CSRC / unit}")
     seen: dict[Path, None] = {}
     todo = [CSRC / unit]
     while todo:
@@ -107,7 +111,7 @@ def main(argv: list[str]) -> int:
     for spec in argv[6:]:
         name, rest = spec.split("=", 1)
         unit, sym, alg, fdir, wdir = rest.split(":")
-        targets[name] = (unit, sym, int(alg), fdir, wdir)
+        targets[name] = (UNITS.get(unit, unit), sym, int(alg), fdir, wdir)
     res = traffic_summary(cfd, cwd, copy_bytes, targets)
     Path(out).write_text(json.dumps(res, indent=1) + "\n")
     print(json.dumps({k: v.get("ratio") for k, v in res.items() if k != "_calibration"}))
