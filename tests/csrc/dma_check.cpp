@@ -504,23 +504,28 @@ static void check_fused() {
 // --------------------------------------------------------------------------- small-grid chunk_fwd_h
 
 // The register-staged small-grid kernel (chunk_fwd_h_small.h): the memory
-// waves' loads cover each tile's 8-element pieces exactly once, from inside the
-// chunk's token block and the V-tile, into aligned slots of the padded LDS
-// tiles; the state waves' out-buffer writes cover the h and v_new tiles exactly
-// once, conflict-free per instruction; the memory waves' 16-byte out-buffer
-// reads and their stores cover the same tiles exactly once.
-template <int K, int V, int NW, bool DELTA>
+// waves' loads cover each tile's 16-byte pieces (8 bf16 or 4 fp32) exactly
+// once, from inside the chunk's token block and the V-tile, into aligned slots
+// of the padded LDS tiles (fp32 k / w pieces as 8-byte bf16 hi and lo halves
+// at the same offset of two tiles); the state waves' out-buffer writes cover
+// the h and v_new tiles exactly once, conflict-free per instruction; the
+// memory waves' 16-byte out-buffer reads and their stores cover the same tiles
+// exactly once.
+template <int K, int V, int NW, bool DELTA, int EB = 2>
 static void check_small() {
-  using C = pipe::SCfg<K, NW, DELTA>;
+  using C = pipe::SCfg<K, NW, DELTA, EB>;
+  constexpr int VE = C::kVE;
   char what[128];
-  std::snprintf(what, sizeof what, "small chunk_fwd_h K=%d V=%d NW=%d delta=%d", K, V, NW, DELTA);
+  std::snprintf(what, sizeof what, "small chunk_fwd_h K=%d V=%d NW=%d delta=%d %s", K, V, NW, DELTA,
+                EB == 4 ? "fp32" : "bf16");
+  CHECK(C::kFits && C::kLds <= 160 * 1024, "%s: LDS budget", what);
   {
     std::vector<std::pair<int, int>> reg;
     for (int s = 0; s < 2; ++s) {
       const int base = s * C::kStageB;
-      reg.push_back({base, base + C::kKTileB});
-      if (DELTA) reg.push_back({base + C::kKTileB, base + 2 * C::kKTileB});
-      const int ub = base + C::kKTileB * (DELTA ? 2 : 1);
+      for (int t = 0; t < (DELTA ? 2 : 1) * (C::kSplit ? 2 : 1); ++t)  // k hi[, lo][, w hi[, lo]]
+        reg.push_back({base + t * C::kKTileB, base + (t + 1) * C::kKTileB});
+      const int ub = base + C::kKPartB * (DELTA ? 2 : 1);
       reg.push_back({ub, ub + C::kUTileB});
       reg.push_back({ub + C::kUTileB, ub + C::kUTileB + 65 * 4});  // 64 factors + e^{g_last}
       CHECK(ub + C::kUTileB + C::kGateB == base + C::kStageB, "%s: stage %d size", what, s);
@@ -536,18 +541,22 @@ static void check_small() {
               what, i, j);
     }
   }
-  // Loads: (tile width n, pieces per lane, LDS pitch in elements, LDS tile bytes).
-  const int tiles[2][4] = {{K, C::kKLoads, C::kKPitch, C::kKTileB}, {C::kCols, C::kULoads, C::kUPitch, C::kUTileB}};
+  // Loads: (tile width n, pieces per lane, LDS pitch in elements, bytes per
+  // staged element, bytes written per piece, LDS tile bytes).  k / w are
+  // staged as bf16 (fp32: 4 elements -> 8 bytes in the hi tile and 8 in the
+  // lo tile, kKTileB further on); u in the input type.
+  const int tiles[2][6] = {{K, C::kKLoads, C::kKPitch, 2, VE * 2, C::kKTileB},
+                           {C::kCols, C::kULoads, C::kUPitch, EB, 16, C::kUTileB}};
   for (const auto& t : tiles) {
-    const int n = t[0], per = t[1], pitch = t[2], tb = t[3];
-    Cover cv(64, n / 8);
+    const int n = t[0], per = t[1], pitch = t[2], sb = t[3], wb = t[4], tb = t[5];
+    Cover cv(64, n / VE);
     for (int m = 0; m < C::kML; ++m)
       for (int it = 0; it < per; ++it) {
-        const int row = hl::spiece_row(m, it, n, C::kML), col = hl::spiece_col(m, n);
-        CHECK(col % 8 == 0 && col + 8 <= n, "%s: piece column %d outside [0, %d)", what, col, n);
-        cv.add(row, col / 8, what);
-        const int a = (row * pitch + col) * 2;
-        CHECK(a % 16 == 0 && a + 16 <= tb, "%s: LDS slot %d of a %d-byte tile", what, a, tb);
+        const int row = hl::spiece_row(m, it, n, C::kML, VE), col = hl::spiece_col(m, n, VE);
+        CHECK(col % VE == 0 && col + VE <= n, "%s: piece column %d outside [0, %d)", what, col, n);
+        cv.add(row, col / VE, what);
+        const int a = (row * pitch + col) * sb;
+        CHECK(a % wb == 0 && a + wb <= tb && col * sb + wb <= n * sb, "%s: LDS slot %d of a %d-byte tile", what, a, tb);
       }
     cv.exactly_once(what);
   }
@@ -555,14 +564,16 @@ static void check_small() {
   for (const Shape& sh : kShapes) {
     const int64_t NT = sh.T / 64, b = sh.B - 1, hh = sh.H - 1, c = NT - 1, v0 = V - C::kCols;
     const int64_t tok_k = sh.H * K, tok_v = sh.H * V;
-    const int64_t kmax = ((b * sh.T + c * 64 + hl::spiece_row(C::kML - 1, C::kKLoads - 1, K, C::kML)) * sh.H + hh) * K +
-                         hl::spiece_col(C::kML - 1, K) + 8;
+    int64_t kmax = 0, umax = 0, hmax = 0, vmax = 0;
+    for (int m = 0; m < C::kML; ++m)
+      for (int it = 0; it < C::kKLoads; ++it)
+        kmax = std::max(kmax, ((b * sh.T + c * 64 + hl::spiece_row(m, it, K, C::kML, VE)) * sh.H + hh) * K +
+                                  hl::spiece_col(m, K, VE) + VE);
     CHECK(kmax <= sh.B * sh.T * sh.H * K, "%s: k / w load past the tensor", what);
-    int64_t umax = 0, hmax = 0, vmax = 0;
     for (int m = 0; m < C::kML; ++m)
       for (int it = 0; it < C::kULoads; ++it)
-        umax = std::max(umax, ((b * sh.T + c * 64 + hl::spiece_row(m, it, C::kCols, C::kML)) * sh.H + hh) * V + v0 +
-                                  hl::spiece_col(m, C::kCols) + 8);
+        umax = std::max(umax, ((b * sh.T + c * 64 + hl::spiece_row(m, it, C::kCols, C::kML, VE)) * sh.H + hh) * V + v0 +
+                                  hl::spiece_col(m, C::kCols, VE) + VE);
     CHECK(umax <= sh.B * sh.T * sh.H * V, "%s: u load past the tensor", what);
     for (int p = 0; p < K * C::kCols / 4; ++p)
       hmax = std::max(hmax, ((b * NT + c) * sh.H + hh) * K * V + (int64_t)hl::sout_row(p, C::kCols) * V + v0 +
@@ -572,7 +583,7 @@ static void check_small() {
       vmax = std::max(vmax, ((b * sh.T + c * 64 + hl::sout_row(p, C::kCols)) * sh.H + hh) * V + v0 +
                                 hl::sout_col(p, C::kCols) + 4);
     CHECK(vmax <= sh.B * sh.T * sh.H * V, "%s: v_new store past the tensor", what);
-    CHECK((63 * tok_k + K) * 2 < (INT64_C(1) << 32) && (63 * tok_v + V) * 2 < (INT64_C(1) << 32),
+    CHECK((63 * tok_k + K) * EB < (INT64_C(1) << 32) && (63 * tok_v + V) * EB < (INT64_C(1) << 32),
           "%s: per-lane load offsets past 32 bits", what);
   }
   // Out buffers: state writes, memory reads, stores.
@@ -1153,6 +1164,13 @@ int main() {
   check_small<128, 128, 1, true>();
   check_small<64, 64, 4, true>();
   check_small<64, 128, 4, false>();
+  // fp32 inputs (chunk_fwd_h_f32.hip): every form whose stages fit in LDS.
+  check_small<64, 64, 2, true, 4>();
+  check_small<64, 64, 2, false, 4>();
+  check_small<64, 128, 2, true, 4>();
+  check_small<128, 64, 2, false, 4>();
+  check_small<128, 128, 2, false, 4>();
+  static_assert(!pipe::SCfg<128, 2, true, 4>::kFits, "fp32 K = 128 delta form stays on the register kernel");
 #define F_ALL(K, V)                   \
   check_fused<K, V, true, true>();    \
   check_fused<K, V, true, false>();   \

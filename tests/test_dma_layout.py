@@ -106,8 +106,8 @@ MUTATIONS = [
      "fused: w / u DMA three chunks ahead (overwrites a slot still in use)"),
     ("pipe_cfg.h", "  static constexpr int kKqLead = 1;", "  static constexpr int kKqLead = 2;",
      "fused: k / q DMA two chunks ahead (overwrites a slot still in use)"),
-    ("h_layout.h", "THM_HD constexpr int spiece_row(int m, int it, int n, int ml) { return m / (n / 8) + it * (ml / (n / 8)); }",
-     "THM_HD constexpr int spiece_row(int m, int it, int n, int ml) { return m / (n / 8) + it * (ml / (n / 4)); }",
+    ("h_layout.h", "THM_HD constexpr int spiece_row(int m, int it, int n, int ml, int e = 8) { return m / (n / e) + it * (ml / (n / e)); }",
+     "THM_HD constexpr int spiece_row(int m, int it, int n, int ml, int e = 8) { return m / (n / e) + it * (ml / (2 * n / e)); }",
      "small chunk_fwd_h: load pieces at the wrong row stride"),
     ("h_layout.h", "  return (16 * blk + 4 * (lane >> 4) + r) * pitch + 16 * wq + (lane & 15);",
      "  return (16 * blk + 4 * (lane >> 4) + r) * pitch + 16 * wq + (lane & 7);",

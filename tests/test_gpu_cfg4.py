@@ -163,6 +163,26 @@ def test_cfg4_fused_forward(chain):
         assert dev_ <= 1e-2 * (1 + float(ref.float().abs().max())), f"fused {what}: max |diff| {dev_:.3e}"
 
 
+def test_cfg4_fused_forward_a_full(chain):
+    # The fused kernel's A form (v_new = A (beta (v - e^g k S)), w and u never
+    # formed) at full size: every o, v_new and final-state element against the
+    # separate kernels, and one sampled head's whole sequence against the
+    # token-level gated delta rule.
+    from theorem_amd.chain import chunk_fwd_fused_a
+    d = chain
+    o, vn, ht = chunk_fwd_fused_a(d["q"], d["k"], d["v"], d["beta"], d["A"], d["g"], d["scale"], None, True, True)
+    torch.cuda.synchronize()
+    for what, got, ref in (("o", o, d["o"]), ("v_new", vn, d["vn"]), ("final state", ht, d["ht"])):
+        dev_ = float((got.float() - ref.float()).abs().max())
+        assert dev_ <= 1e-2 * (1 + float(ref.float().abs().max())), f"A form {what}: max |diff| {dev_:.3e}"
+    b, hh = HEADS[2]
+    sl = lambda t: np_(t[b:b + 1, :, hh:hh + 1])  # noqa: E731
+    a = np.diff(sl(d["g"]).reshape(1, T // BT, BT, 1), axis=2, prepend=0.0).reshape(1, T, 1)
+    eo, eS = odn.gated_delta_rule_tokens(sl(d["q"]), sl(d["k"]), sl(d["v"]), sl(d["beta"]), a, d["scale"])
+    assert_close(o[b:b + 1, :, hh:hh + 1], eo, 1e-2, 1e-2, f"A form o (b={b}, head={hh})")
+    assert_close(ht[b:b + 1, hh:hh + 1], eS, 1e-2, 1e-2, f"A form final state (b={b}, head={hh})")
+
+
 def test_cfg4_wy_fwd_full(chain):
     # The fused WY kernel at full size: bit-identical to A-builder + recompute_w_u
     # (the same fp32 A on chip), and within tolerance of the chain's w, u (whose A

@@ -20,10 +20,6 @@
 #include "chunk_fwd_h_reg.h"
 #include "chunk_fwd_h_small.h"
 
-// State waves per workgroup of the small-grid kernel (V-tile of 32 columns).
-// At config 3 (B=2, T=1024, H=3, K=V=64), per launch with HIP events: 1
-// state wave 15.9 us, 2 15.6, 4 21.6; the register kernel 26.8.
-constexpr int kHSmallNW = 2;
 #include "pipe_cfg.h"
 
 namespace thm {
@@ -361,7 +357,7 @@ hipError_t launch_kv(const void* k, const void* w, const void* vu, const void* g
   if constexpr (std::is_same<IT, bf16>::value) {
     if (B * H * (V / kHBV) >= kHDmaMinGrid)
       return launch_h_dma<K, V, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
-    return launch_h_small<K, V, kHSmallNW, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
+    return launch_h_small<bf16, K, V, kHSmallNW, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
   }
   return launch_h<IT, K, V, DELTA>(k, w, vu, g, h0, h, vnew, ht, B, T, H, s);
 }

@@ -1,9 +1,11 @@
-// Gated DeltaNet inter-chunk state recurrence, bf16 inputs on small grids
-// (fewer workgroups than CUs): a role-split kernel for the chunk latency.
-// Included by chunk_fwd_h.hip.
+// Gated DeltaNet inter-chunk state recurrence on small grids (fewer
+// workgroups than CUs): a role-split kernel for the chunk latency.  Included
+// by chunk_fwd_h.hip (bf16 inputs) and chunk_fwd_h_f32.hip (fp32 inputs).
 //
 // The math is the register kernel's (chunk_fwd_h_reg.h), operation for
-// operation, so h, v_new and the final state are bit-identical to it:
+// operation, so h, v_new and the final state are bit-identical to it (fp32
+// inputs: k and w staged as bf16 hi + lo, S and the gated v_new split the
+// same way, three MFMAs per product):
 //   reference form (DELTA = false; vu = v)                kernels/chunk_fwd_h/
 //     S <- e^{g_last} S + k_c^T (v_c e^{g_last - g_c});  h[c] = S      reference.py:50-97
 //   delta form (DELTA = true; vu = u)
@@ -46,14 +48,22 @@ namespace {
 
 using pipe::SCfg;
 
-template <int K, int V, int NW, bool DELTA, bool HAS_G>
+// State waves per workgroup (V-tile of 32 columns).  At config 3 (B=2,
+// T=1024, H=3, K=V=64, bf16), per launch with HIP events: 1 state wave
+// 15.9 us, 2 15.6, 4 21.6; the register kernel 26.8.
+constexpr int kHSmallNW = 2;
+
+template <typename IT, int K, int V, int NW, bool DELTA, bool HAS_G>
 __global__ void __launch_bounds__(128 * NW)
-chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
-                         const bf16* __restrict__ vu, const float* __restrict__ g,
+chunk_fwd_h_small_kernel(const IT* __restrict__ k, const IT* __restrict__ w,
+                         const IT* __restrict__ vu, const float* __restrict__ g,
                          const float* __restrict__ h0, float* __restrict__ hout,
-                         bf16* __restrict__ vnew, float* __restrict__ ht, int64_t T, int64_t H,
+                         IT* __restrict__ vnew, float* __restrict__ ht, int64_t T, int64_t H,
                          int64_t NT, int64_t BH) {
-  using C = SCfg<K, NW, DELTA>;
+  constexpr int EB = (int)sizeof(IT);
+  using C = SCfg<K, NW, DELTA, EB>;
+  static_assert(C::kFits, "LDS budget");
+  constexpr bool SPLIT = C::kSplit;
   constexpr int KB = K / 16;
   constexpr int NVT = V / C::kCols;
   __shared__ __attribute__((aligned(16))) char lds[C::kLds];
@@ -66,13 +76,16 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
   const int grp = lane >> 4;
   const int li = lane & 15;
 
+  // Stage s: k hi[, lo], w hi[, lo] (delta form), u, gate factors.  The lo
+  // tile of a split operand follows its hi tile.
   auto st_k = [&](int s) { return reinterpret_cast<bf16*>(lds + s * C::kStageB); };
-  auto st_w = [&](int s) { return reinterpret_cast<bf16*>(lds + s * C::kStageB + C::kKTileB); };
+  auto st_w = [&](int s) { return reinterpret_cast<bf16*>(lds + s * C::kStageB + C::kKPartB); };
+  auto lo_of = [](const bf16* hi) { return hi + C::kKTileB / 2; };
   auto st_u = [&](int s) {
-    return reinterpret_cast<bf16*>(lds + s * C::kStageB + C::kKTileB * (DELTA ? 2 : 1));
+    return reinterpret_cast<IT*>(lds + s * C::kStageB + C::kKPartB * (DELTA ? 2 : 1));
   };
   auto st_f = [&](int s) {
-    return reinterpret_cast<float*>(lds + s * C::kStageB + C::kKTileB * (DELTA ? 2 : 1) + C::kUTileB);
+    return reinterpret_cast<float*>(lds + s * C::kStageB + C::kKPartB * (DELTA ? 2 : 1) + C::kUTileB);
   };
   char* const hob = lds + 2 * C::kStageB;     // out buffers: h [2][kHOutB]
   char* const vob = hob + 2 * C::kHOutB;      // v_new [2][kVOutB]
@@ -100,7 +113,7 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
     for (int64_t c = 0; c < NT; ++c) {
       const int s = (int)(c & 1);
       const bf16* const ks = st_k(s);
-      const bf16* const us = st_u(s);
+      const IT* const us = st_u(s);
       const float* const fs = st_f(s);
       char* const ho = hob + s * C::kHOutB;
       if constexpr (DELTA) {
@@ -113,26 +126,39 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
       f32x4 vn[4];
 #pragma unroll
       for (int jb = 0; jb < 4; ++jb) {
-        const bf16x4 u4 = ds_read_tr16(us + (16 * jb + 4 * grp + (li >> 2)) * C::kUPitch + 16 * wv + 4 * (li & 3));
+        if constexpr (SPLIT) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vn[jb][r] = to_f32(u4[r]);
+          for (int r = 0; r < 4; ++r) vn[jb][r] = us[(16 * jb + 4 * grp + r) * C::kUPitch + ucol];
+        } else {
+          const bf16x4 u4 = ds_read_tr16(us + (16 * jb + 4 * grp + (li >> 2)) * C::kUPitch + 16 * wv + 4 * (li & 3));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vn[jb][r] = to_f32(u4[r]);
+        }
       }
       if constexpr (DELTA) {
         // P1: B operand = S pairs (kappa blocks 2t, 2t+1) in paired order.
         const bf16* const ws = st_w(s);
-        bf16x8 sh[K / 32];
+        bf16x8 sh[K / 32], sl[SPLIT ? K / 32 : 1];
 #pragma unroll
         for (int t = 0; t < K / 32; ++t) {
           const float f[8] = {S[2 * t][0], S[2 * t][1], S[2 * t][2], S[2 * t][3],
                               S[2 * t + 1][0], S[2 * t + 1][1], S[2 * t + 1][2], S[2 * t + 1][3]};
-          sh[t] = to_bf16x8(f);
+          if constexpr (SPLIT) split_bf16x8(f, sh[t], sl[t]);
+          else sh[t] = to_bf16x8(f);
         }
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
           f32x4 a = zero4();
           const bf16* const wrow = ws + (16 * jb + li) * C::kKPitch;
 #pragma unroll
-          for (int t = 0; t < K / 32; ++t) a = mfma16x16x32(load8_paired(wrow, 32 * t), sh[t], a);
+          for (int t = 0; t < K / 32; ++t) {
+            const bf16x8 wf = load8_paired(wrow, 32 * t);
+            a = mfma16x16x32(wf, sh[t], a);
+            if constexpr (SPLIT) {
+              a = mfma16x16x32(wf, sl[t], a);
+              a = mfma16x16x32(load8_paired(lo_of(wrow), 32 * t), sh[t], a);
+            }
+          }
           vn[jb] -= a;
         }
         char* const vo = vob + s * C::kVOutB;
@@ -141,7 +167,7 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
       }
       // P2: S = e^{g_last} S + k^T (v_new e^{g_last - g}), the factors staged by
       // the memory waves.
-      bf16x8 vh[2];
+      bf16x8 vh[2], vl[SPLIT ? 2 : 1];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const f32x4 fa = *reinterpret_cast<const f32x4*>(fs + 32 * t + 4 * grp);
@@ -152,7 +178,8 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
           f[r] = vn[2 * t][r] * fa[r];
           f[4 + r] = vn[2 * t + 1][r] * fb[r];
         }
-        vh[t] = to_bf16x8(f);
+        if constexpr (SPLIT) split_bf16x8(f, vh[t], vl[t]);
+        else vh[t] = to_bf16x8(f);
       }
       const float decay = fs[64];
 #pragma unroll
@@ -160,8 +187,13 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
         S[kb] *= decay;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const bf16x8 kf = frag_tr(ks, C::kKPitch, tr_row_paired(32 * t, 0), tr_row_paired(32 * t, 1), 16 * kb);
+          const int r0 = tr_row_paired(32 * t, 0), r1 = tr_row_paired(32 * t, 1);
+          const bf16x8 kf = frag_tr(ks, C::kKPitch, r0, r1, 16 * kb);
           S[kb] = mfma16x16x32(kf, vh[t], S[kb]);
+          if constexpr (SPLIT) {
+            S[kb] = mfma16x16x32(kf, vl[t], S[kb]);
+            S[kb] = mfma16x16x32(frag_tr(lo_of(ks), C::kKPitch, r0, r1, 16 * kb), vh[t], S[kb]);
+          }
         }
       }
       if constexpr (!DELTA) {
@@ -182,19 +214,20 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
   // ------------------------------------------------------------------ memory waves
   const int m = wv - NW;
   const int tid = (int)threadIdx.x - C::kML;  // 0 .. kML - 1
-  // Loads: piece it of this lane is row hl::spiece_row(tid, it, n, kML),
-  // elements hl::spiece_col(tid, n) .. + 7 of the k / w (n = K) or u / v
-  // (n = kCols) tile; successive pieces are kKRows / kURows rows apart.
+  // Loads: piece it of this lane is row hl::spiece_row(tid, it, n, kML, kVE),
+  // elements hl::spiece_col(tid, n, kVE) .. + kVE - 1 of the k / w (n = K) or
+  // u / v (n = kCols) tile; successive pieces are kKRows / kURows rows apart.
+  constexpr int VE = C::kVE;
   constexpr int kKRows = C::kML / C::kKCPR, kURows = C::kML / C::kUCPR;
-  const int kj0 = hl::spiece_row(tid, 0, K, C::kML), kcol = hl::spiece_col(tid, K);
-  const int uj0 = hl::spiece_row(tid, 0, C::kCols, C::kML), ucol0 = hl::spiece_col(tid, C::kCols);
-  const uint32_t koff = (uint32_t)(kj0 * tok_k + kcol) * 2;        // bytes from the chunk base
-  const uint32_t kstep = (uint32_t)(kKRows * tok_k) * 2;
-  const uint32_t uoff = (uint32_t)(uj0 * tok_v + v0 + ucol0) * 2;
-  const uint32_t ustep = (uint32_t)(kURows * tok_v) * 2;
-  const int64_t kc0 = ((b * T) * H + hh) * K * 2;  // bytes: chunk 0 of this (b, head)
-  const int64_t uc0 = ((b * T) * H + hh) * V * 2;
-  const int64_t kcs = 64 * tok_k * 2, ucs = 64 * tok_v * 2;
+  const int kj0 = hl::spiece_row(tid, 0, K, C::kML, VE), kcol = hl::spiece_col(tid, K, VE);
+  const int uj0 = hl::spiece_row(tid, 0, C::kCols, C::kML, VE), ucol0 = hl::spiece_col(tid, C::kCols, VE);
+  const uint32_t koff = (uint32_t)(kj0 * tok_k + kcol) * EB;        // bytes from the chunk base
+  const uint32_t kstep = (uint32_t)(kKRows * tok_k) * EB;
+  const uint32_t uoff = (uint32_t)(uj0 * tok_v + v0 + ucol0) * EB;
+  const uint32_t ustep = (uint32_t)(kURows * tok_v) * EB;
+  const int64_t kc0 = ((b * T) * H + hh) * K * EB;  // bytes: chunk 0 of this (b, head)
+  const int64_t uc0 = ((b * T) * H + hh) * V * EB;
+  const int64_t kcs = 64 * tok_k * EB, ucs = 64 * tok_v * EB;
   auto cbytes = [](const void* p, int64_t off) { return reinterpret_cast<const char*>(p) + off; };
 
   // Two register sets: the loads of chunk c + 3 are issued during chunk c and
@@ -221,18 +254,27 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
     if constexpr (HAS_G) r.g = g[(b * T + c * 64 + lane) * H + hh];
     else r.g = 0.f;
   };
+  // A k / w piece into its tile: as loaded (bf16), or split into bf16 hi and
+  // lo halves at the same offset of the hi and lo tiles (fp32).
+  auto put_piece = [&](bf16* tile, int off, u32x4 v) {
+    if constexpr (SPLIT) {
+      float f[4];
+      unpack16(v, f, 0.f);
+      lds_put4(tile + off, tile + C::kKTileB / 2 + off, f, true);
+    } else {
+      *reinterpret_cast<u32x4*>(tile + off) = v;
+    }
+  };
   auto commit = [&](const Regs& r, int s) {
     bf16* const ks = st_k(s);
 #pragma unroll
-    for (int it = 0; it < C::kKLoads; ++it)
-      *reinterpret_cast<u32x4*>(ks + (kj0 + it * kKRows) * C::kKPitch + kcol) = r.k[it];
+    for (int it = 0; it < C::kKLoads; ++it) put_piece(ks, (kj0 + it * kKRows) * C::kKPitch + kcol, r.k[it]);
     if constexpr (DELTA) {
       bf16* const ws = st_w(s);
 #pragma unroll
-      for (int it = 0; it < C::kKLoads; ++it)
-        *reinterpret_cast<u32x4*>(ws + (kj0 + it * kKRows) * C::kKPitch + kcol) = r.w[it];
+      for (int it = 0; it < C::kKLoads; ++it) put_piece(ws, (kj0 + it * kKRows) * C::kKPitch + kcol, r.w[it]);
     }
-    bf16* const us = st_u(s);
+    IT* const us = st_u(s);
 #pragma unroll
     for (int it = 0; it < C::kULoads; ++it)
       *reinterpret_cast<u32x4*>(us + (uj0 + it * kURows) * C::kUPitch + ucol0) = r.u[it];
@@ -277,13 +319,18 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
     }
     if constexpr (DELTA) {
       if (vnew) {  // uniform
-        bf16* const vb = vnew + ((b * T + c * 64) * H + hh) * V + v0;
+        IT* const vb = vnew + ((b * T + c * 64) * H + hh) * V + v0;
 #pragma unroll
         for (int i = 0; i < kVPieces; ++i) {
           const int p = i * C::kML + tid;
-          bf16x4 o;
-          o[0] = (bf16)vv[i][0]; o[1] = (bf16)vv[i][1]; o[2] = (bf16)vv[i][2]; o[3] = (bf16)vv[i][3];
-          *reinterpret_cast<bf16x4*>(vb + hl::sout_row(p, C::kCols) * tok_v + hl::sout_col(p, C::kCols)) = o;
+          IT* const dst = vb + hl::sout_row(p, C::kCols) * tok_v + hl::sout_col(p, C::kCols);
+          if constexpr (SPLIT) {
+            *reinterpret_cast<f32x4*>(dst) = vv[i];
+          } else {
+            bf16x4 o;
+            o[0] = (bf16)vv[i][0]; o[1] = (bf16)vv[i][1]; o[2] = (bf16)vv[i][2]; o[3] = (bf16)vv[i][3];
+            *reinterpret_cast<bf16x4*>(dst) = o;
+          }
         }
       }
     }
@@ -312,16 +359,16 @@ chunk_fwd_h_small_kernel(const bf16* __restrict__ k, const bf16* __restrict__ w,
   if (NT > 0) store_out(NT - 1, (int)((NT - 1) & 1));
 }
 
-template <int K, int V, int NW, bool DELTA>
+template <typename IT, int K, int V, int NW, bool DELTA>
 hipError_t launch_h_small(const void* k, const void* w, const void* vu, const void* g, const void* h0,
                           void* h, void* vnew, void* ht, int64_t B, int64_t T, int64_t H, hipStream_t s) {
   const int64_t NT = T / 64;
   const int64_t BH = B * H;
   const dim3 grid((unsigned)(BH * (V / (16 * NW))));
-#define THM_H_SMALL_LAUNCH(HG)                                                                          \
-  hipLaunchKernelGGL((chunk_fwd_h_small_kernel<K, V, NW, DELTA, HG>), grid, dim3(128 * NW), 0, s,   \
-                     (const bf16*)k, (const bf16*)w, (const bf16*)vu, (const float*)g,                 \
-                     (const float*)h0, (float*)h, (bf16*)vnew, (float*)ht, T, H, NT, BH)
+#define THM_H_SMALL_LAUNCH(HG)                                                                            \
+  hipLaunchKernelGGL((chunk_fwd_h_small_kernel<IT, K, V, NW, DELTA, HG>), grid, dim3(128 * NW), 0, s, \
+                     (const IT*)k, (const IT*)w, (const IT*)vu, (const float*)g,                         \
+                     (const float*)h0, (float*)h, (IT*)vnew, (float*)ht, T, H, NT, BH)
   if (g) THM_H_SMALL_LAUNCH(true);
   else THM_H_SMALL_LAUNCH(false);
 #undef THM_H_SMALL_LAUNCH

@@ -231,11 +231,11 @@ THM_HD inline BhTile xcd_tile(int64_t blk, int64_t BH, int nvt) {
 }
 
 // Small-grid chunk_fwd_h kernel (chunk_fwd_h_small.h).  Memory lane m of ml
-// loads 8-element pieces of a [64 x n] bf16 tile (k, w: n = K; u: n = the
-// V-tile width): its piece it is row spiece_row(m, it, n, ml), elements
-// spiece_col(m, n) .. + 7.
-THM_HD constexpr int spiece_row(int m, int it, int n, int ml) { return m / (n / 8) + it * (ml / (n / 8)); }
-THM_HD constexpr int spiece_col(int m, int n) { return (m % (n / 8)) * 8; }
+// loads 16-byte pieces of e elements (8 bf16 or 4 fp32) of a [64 x n] tile
+// (k, w: n = K; u: n = the V-tile width): its piece it is row
+// spiece_row(m, it, n, ml, e), elements spiece_col(m, n, e) .. + e - 1.
+THM_HD constexpr int spiece_row(int m, int it, int n, int ml, int e = 8) { return m / (n / e) + it * (ml / (n / e)); }
+THM_HD constexpr int spiece_col(int m, int n, int e = 8) { return (m % (n / e)) * e; }
 // Out buffer (fp32, row-major, `pitch` floats per row): lane `lane` of state
 // wave wq writes rows 16 blk + 4 (lane / 16) + r (r = 0..3) of column
 // 16 wq + lane % 16, one float each.

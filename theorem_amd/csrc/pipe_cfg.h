@@ -111,20 +111,25 @@ struct FCfg {
 };
 
 // ---------------------------------------------------------------------------
-// chunk_fwd_h, small-grid bf16 kernel (chunk_fwd_h_small.h): NW state waves and
+// chunk_fwd_h, small-grid kernel (chunk_fwd_h_small.h): NW state waves and
 // NW memory waves per workgroup, a V-tile of 16 NW columns; per stage the
 // padded k, w (delta form) and u tiles and the chunk's gate factors, then two
-// fp32 out buffers each for h and v_new.
-template <int K, int NW, bool DELTA>
+// fp32 out buffers each for h and v_new.  EB = bytes per input element: bf16
+// (2) stages k and w as they are, fp32 (4) as bf16 hi and lo tiles (the
+// register kernel's split), and u in its own type.
+template <int K, int NW, bool DELTA, int EB = 2>
 struct SCfg {
+  static constexpr bool kSplit = EB == 4;
   static constexpr int kThreads = 128 * NW;
   static constexpr int kCols = 16 * NW;                // V-tile width
+  static constexpr int kVE = 16 / EB;                  // input elements per 16-byte piece
   static constexpr int kKPitch = K + 8;                // bf16 elements per k / w row (16-byte pad)
-  static constexpr int kUPitch = kCols + 8;            // bf16 elements per u / v row of the V-tile
-  static constexpr int kKTileB = 64 * kKPitch * 2;     // bytes
-  static constexpr int kUTileB = 64 * kUPitch * 2;
+  static constexpr int kUPitch = kCols + kVE;          // input elements per u / v row of the V-tile
+  static constexpr int kKTileB = 64 * kKPitch * 2;     // bytes of one bf16 k / w tile
+  static constexpr int kKPartB = kKTileB * (kSplit ? 2 : 1);  // k (or w): hi[, lo]
+  static constexpr int kUTileB = 64 * kUPitch * EB;
   static constexpr int kGateB = 80 * 4;                // 64 factors e^{g_last - g_j}, e^{g_last}, pad
-  static constexpr int kStageB = kKTileB * (DELTA ? 2 : 1) + kUTileB + kGateB;
+  static constexpr int kStageB = kKPartB * (DELTA ? 2 : 1) + kUTileB + kGateB;
   // Out buffers: fp32, row-major, kOutPitch floats per row.  The state waves
   // write single floats, 16 lanes of a row-quad group 4 rows apart; a pitch of
   // 4 mod 16 floats puts those 4 rows 16 banks apart (conflict-free).
@@ -132,14 +137,16 @@ struct SCfg {
   static constexpr int kHOutB = K * kOutPitch * 4;
   static constexpr int kVOutB = DELTA ? 64 * kOutPitch * 4 : 0;
   static constexpr int kLds = 2 * kStageB + 2 * (kHOutB + kVOutB);
-  // memory-wave loads per lane per chunk (16-byte pieces of 8 bf16)
+  static constexpr bool kFits = kLds <= 160 * 1024;    // fp32 with K = 128 in the delta form does not
+  // memory-wave loads per lane per chunk (16-byte pieces of kVE elements)
   static constexpr int kML = 64 * NW;                  // memory lanes
-  static constexpr int kKCPR = K / 8;                  // pieces per k / w row
+  static constexpr int kKCPR = K / kVE;                // pieces per k / w row
   static constexpr int kKLoads = 64 * kKCPR / kML;
-  static constexpr int kUCPR = kCols / 8;              // pieces per u row of the V-tile
+  static constexpr int kUCPR = kCols / kVE;            // pieces per u row of the V-tile
   static constexpr int kULoads = 64 * kUCPR / kML;
+  static_assert(EB == 2 || EB == 4, "bf16 or fp32 inputs");
   static_assert(NW == 1 || NW == 2 || NW == 4, "state waves");
-  static_assert(kStageB % 16 == 0 && kLds <= 160 * 1024, "LDS budget");
+  static_assert(kStageB % 16 == 0, "16-byte aligned stages");
   static_assert(64 * kKCPR % kML == 0 && kML % kKCPR == 0 && kML % kUCPR == 0, "load split");
 };
 
