@@ -344,6 +344,31 @@ def test_h_fp32_deep_prefetch(dev, K, V, form):
         assert_close(ht, eht, 1e-3, 1e-3, f"final fp32 {form} K={K} V={V} T={T}")
 
 
+# fp32 grids under 256 workgroups run the role-split small-grid kernel where
+# its stages fit in LDS (all but K = 128 in the delta form).  The reference
+# form at every K, V, with and without gates and initial state;
+# T = 64 * (1 .. 5) covers the odd / even chunk counts of its memory waves'
+# two-chunk loop and the one-chunk case.
+@pytest.mark.parametrize("K,V", KV)
+@pytest.mark.parametrize("form", ["reference", "reference_plain"])
+def test_h_fp32_small_grid_reference_form(dev, K, V, form):
+    B, H = 2, 3
+    assert B * H * (V // 64) < 256
+    for T in (64, 128, 192, 256, 320):
+        d = configs.make_h_inputs(B, T, H, K, V, seed=14, device=dev, dtype=torch.float32, h0_std=0.1)
+        plain = form.endswith("plain")
+        g = None if plain else d["g"]
+        h0 = None if plain else d["h0"]
+        gk = np_(g) if g is not None else None
+        h0k = np_(h0) if h0 is not None else None
+        h, ht = chunk_fwd_h.custom_kernel(dict(k=d["k"], v=d["u"], g=g, initial_state=h0, output_final_state=True))
+        sync()
+        pre, _, eht = odn.chunk_fwd_h_delta(np_(d["k"]), np.zeros_like(np_(d["w"])), np_(d["u"]), gk, h0=h0k)
+        eh = np.concatenate([pre[:, 1:], eht[:, None]], axis=1)
+        assert_close(h, eh, 1e-4, 1e-4, f"h fp32 {form} K={K} V={V} T={T}")
+        assert_close(ht, eht, 1e-4, 1e-4, f"final fp32 {form} K={K} V={V} T={T}")
+
+
 def test_h_dma_pipeline_unaligned_head_count_and_empty(dev):
     # B * H not a multiple of 8 (the plain block mapping) and T = 0 on the DMA path.
     B, T, H, K, V = 1, 128, 260, 64, 64
