@@ -48,6 +48,22 @@ def test_digest_changes_with_a_transitive_header_only(tmp_path, monkeypatch):
     assert profiling.source_digest("chunk_fwd_o.hip") != d0
 
 
+def test_unknown_unit_raises_and_cli_takes_units_keys(tmp_path):
+    # A unit name that is no source file must not hash to the empty digest
+    # (which would mark every summary built from it as matching nothing).
+    with pytest.raises(FileNotFoundError):
+        profiling.source_digest("chunk_fwd_h")
+    calib, kern = tmp_path / "calib", tmp_path / "kern"
+    _counter_csv(calib, [(profiling.COPY_KERNEL, "FETCH_SIZE", 512.0), (profiling.COPY_KERNEL, "WRITE_SIZE", 1024.0)])
+    _counter_csv(kern, [("_ZN3thm6kernelEv", "FETCH_SIZE", 8.0), ("_ZN3thm6kernelEv", "WRITE_SIZE", 4.0)])
+    out = tmp_path / "t.json"
+    spec = f"chunk_fwd_h=chunk_fwd_h:_ZN3thm6kernel:24576:{kern}:{kern}"
+    assert profiling.main(["profiling", "traffic", str(out), str(calib), str(calib), "1048576", spec]) == 0
+    rec = json.loads(out.read_text())["chunk_fwd_h"]
+    assert rec["source_digest"] == profiling.source_digest(profiling.UNITS["chunk_fwd_h"])
+    assert rec["hbm_read_bytes"] == 8 * 1024 * 2 and rec["hbm_write_bytes"] == 4 * 1024
+
+
 def _counter_csv(path: Path, rows):
     path.mkdir(parents=True, exist_ok=True)
     with open(path / "run_counter_collection.csv", "w", newline="") as f:
