@@ -77,6 +77,37 @@ __device__ __forceinline__ void form_L(const bf16x8 (&fh)[4][KS], const bf16x8 (
   }
 }
 
+// form_L for bf16 k with the fragments read from LDS per block (frag(tb, s)
+// returns k[16 tb + li][32 s + 8 grp .. + 7]) instead of held in registers
+// for the whole chunk: the same products in the same order, ~40 fewer VGPRs
+// at K = 128 (the A-builder's pipelined kernel, 4 workgroups per CU).
+template <int SIGN, int KS, typename Frag>
+__device__ __forceinline__ void form_L_lds(Frag frag, const float* sb, const float* sg, float* Lb, int wv) {
+  const int lane = lane_id(), grp = lane >> 4, li = lane & 15;
+#pragma unroll
+  for (int p = 0; p < 10; ++p) {
+    if ((p & 3) != wv) continue;  // wave-uniform
+    constexpr int kIb[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
+    const int ib = kIb[p], jb = p - ib * (ib + 1) / 2;
+    bf16x8 fi[KS], fj[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      fi[s] = frag(ib, s);
+      fj[s] = frag(jb, s);
+    }
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acc = mfma16x16x32(fi[s], fj[s], acc);
+    const int j = 16 * jb + li;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * ib + 4 * grp + r;
+      Lb[p * kBlk + hl::wy_put_off(lane, r)] =
+          (j < i) ? (float)SIGN * sb[i] * acc[r] * fast_exp(sg[i] - sg[j]) : 0.f;
+    }
+  }
+}
+
 // X = (I + L)^{-1} from the L blocks (all four waves; ends with a barrier):
 //   diagonal blocks: wave w, lane c < 16 owns column c of X_ww (16-row
 //   forward substitution), then one barrier;

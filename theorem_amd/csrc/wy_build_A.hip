@@ -119,13 +119,20 @@ wy_build_A_kernel(const IT* __restrict__ k, const float* __restrict__ beta,
 // loads are in flight through form_L and the inversion; the k tile is staged
 // in LDS and the MFMA fragments are read from there.  The arithmetic is the
 // one-tile kernel's, so A is bit-identical.
-// Workgroups per CU: 3.  The k loads go through one 32-bit per-lane offset on
-// a wave-uniform base (h_layout.h o_blk_lane / o_blk_step), which brings the
-// K = 128 form to 159 VGPRs, under the 168-register cap of 3 workgroups
-// (with 64-bit addresses per load it spilled there, and ran at 2): config 4
-// 140 -> 116 us, A bit-identical.  K = 64: 107 us at 3 against 135 at 2.
+// Workgroups per CU: 4.  The inversion's latency chain, not memory, sets this
+// kernel's time (timing-only copies at config 4: 105.4 us; without the
+// inversion 26.6, without the next tile's loads 99.5, without the stores of
+// A 95.2), so the more tiles a CU inverts at once the better:
+//   * the k loads go through one 32-bit per-lane offset on a wave-uniform
+//     base (h_layout.h o_blk_lane / o_blk_step; 64-bit addresses spilled at
+//     3 workgroups): 2 -> 3 per CU, 140 -> 116 us;
+//   * the X and T blocks share the k tile's LDS (31.7 KB per workgroup
+//     instead of 48.6) and form_L reads its k fragments per block
+//     (wy::form_L_lds; 120 VGPRs at K = 128, no scratch): 3 -> 4 per CU,
+//     105.7 -> 96.3 us.  5 per CU spill (140 us).
+// A is bit-identical throughout.
 template <int K>
-constexpr int ab_pipe_wgs_per_cu() { return 3; }
+constexpr int ab_pipe_wgs_per_cu() { return 4; }
 
 template <int K, int SIGN>
 __global__ void __launch_bounds__(kABThreads, ab_pipe_wgs_per_cu<K>())
@@ -139,10 +146,15 @@ wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ bet
   constexpr int kCPR = K / 8;                         // 16-byte chunks per k row
   constexpr int kLoads = kBT * kCPR / kABThreads;     // per thread
   static_assert(kBT * kCPR % kABThreads == 0, "staging split");
-  __shared__ __attribute__((aligned(16))) bf16 ks[kBT * kPitch];
+  // The k tile is read only up to the barrier after form_L and restaged
+  // after the barrier that follows the store of A, so the inversion's X and T
+  // blocks share its LDS.
+  constexpr int kKBytes = kBT * kPitch * 2, kXTBytes = 13 * kBlk * 4;
+  __shared__ __attribute__((aligned(16))) char kxt[kKBytes > kXTBytes ? kKBytes : kXTBytes];
+  bf16* const ks = reinterpret_cast<bf16*>(kxt);
+  float* const Xb = reinterpret_cast<float*>(kxt);
+  float* const Tb = Xb + 10 * kBlk;
   __shared__ float Lb[10 * kBlk];
-  __shared__ float Xb[10 * kBlk];
-  __shared__ float Tb[3 * kBlk];
   __shared__ float sb[kBT], sg[kBT];
 
   const int tid = threadIdx.x;
@@ -151,7 +163,7 @@ wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ bet
   const int grp = lane >> 4, li = lane & 15;
 
   // XCD-aware walk (h_layout.h xcd_tile_order, a bijection of the tiles;
-  // with a grid that is a multiple of 8, 768 on MI355X, sequence index t runs
+  // with a grid that is a multiple of 8, 1024 on MI355X, sequence index t runs
   // on XCD t % 8): the 16 heads of a (b, chunk) share
   // one XCD's L2, so each 64-byte line of beta and g is fetched once, not once
   // per XCD.  Measured traffic 1.108 -> 1.00 of the algorithmic bytes, at
@@ -200,13 +212,9 @@ wy_build_A_pipe_kernel(const bf16* __restrict__ k, const float* __restrict__ bet
     if (tn < tiles) prefetch(tn);  // in flight while tile t computes
     int64_t h;
     const int64_t tok0 = tok_of(t, h);
-    bf16x8 fh[4][KS], fl[4][1];
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-      for (int s = 0; s < KS; ++s) fh[tb][s] = load8(ks + (16 * tb + li) * kPitch + 32 * s + 8 * grp);
-    wy::form_L<SIGN, KS, false>(fh, fl, sb, sg, Lb, wv);
-    lds_barrier();
+    wy::form_L_lds<SIGN, KS>([&](int tb, int s) { return load8(ks + (16 * tb + li) * kPitch + 32 * s + 8 * grp); },
+                             sb, sg, Lb, wv);
+    lds_barrier();  // every wave's k fragment reads are done: X may overwrite ks
     wy::invert_L(Lb, Xb, Tb, wv);  // ends with a barrier
     store_A(Xb, A + (tok0 * H + h) * kBT, H);
 
