@@ -112,6 +112,14 @@ def test_fused_mild_gate_carry(dev, K, V):
     assert_close(o, eo, TOL, TOL, f"fused o K={K} V={V}")
     assert_close(vn, evn, TOL, sc * TOL, f"fused v_new K={K} V={V}")
     assert_close(ht, eht, TOL, sc * TOL, f"fused final state K={K} V={V}")
+    # The generator's own scale (u, h0 / 16, exact): every output is linear in
+    # (u, h0) jointly, so the oracle's values are the ones above / 16, and all
+    # three outputs are held to 1e-2, as chunk_fwd_h's kernels are.
+    o1, vn1, ht1 = chain.chunk_fwd_fused(q, d["k"], d["w"], d["u"] / sc, d["g"], scale, d["h0"] / sc, True, True)
+    torch.cuda.synchronize()
+    assert_close(o1, eo / sc, TOL, TOL, f"fused o, unscaled, K={K} V={V}")
+    assert_close(vn1, evn / sc, TOL, TOL, f"fused v_new, unscaled, K={K} V={V}")
+    assert_close(ht1, eht / sc, TOL, TOL, f"fused final state, unscaled, K={K} V={V}")
 
 
 def _chain_inputs(B, T, H, K, V, seed):
