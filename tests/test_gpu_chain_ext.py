@@ -60,7 +60,7 @@ def test_build_A_vs_oracle(dev, K, dtype, sign, gate):
     assert np.abs(res).max() < 1e-4 * max(1.0, scale)
 
 
-# bf16 grids of at least two tiles per persistent workgroup (3 per CU) run the
+# bf16 grids of at least two tiles per persistent workgroup (4 per CU) run the
 # software-pipelined A-builder: it must equal the one-tile kernel bit for bit
 # (compared on a slice small enough to take the one-tile path) and the oracle.
 @pytest.mark.parametrize("K", [64, 128])
@@ -78,6 +78,22 @@ def test_build_A_pipelined_path(dev, K, sign, gate):
     gk = np_(g[:1, :128]) if g is not None else np.zeros((1, 128, H))
     eA = odn.build_A(kk, np_(beta[:1, :128]), gk, sign=sign)
     assert_close(A[:1, :128], eA, 0, 1e-4 * np.abs(eA).max(), f"A K={K} sign={sign} gate={gate}")
+
+
+@pytest.mark.parametrize("K", [64, 128])
+def test_build_A_pipelined_ragged_tail(dev, K):
+    # 2049 tiles: one more than two per workgroup of the persistent grid (1024
+    # on 256 CUs), so one workgroup takes a third tile.  Each chunk's A depends
+    # on that chunk alone, so the whole tensor must equal the one-tile kernel's
+    # over two slices that each stay under the pipelined path's threshold.
+    B, T, H = 1, 64 * 683, 3
+    k, beta, g = _A_inputs(B, T, H, K, torch.bfloat16, "logsigmoid", seed=8, dev=dev)
+    A = recompute_w_u.build_A(k, beta, g, sign=1)
+    cut = 64 * 600
+    parts = [recompute_w_u.build_A(k[:, s].contiguous(), beta[:, s].contiguous(), g[:, s].contiguous(), sign=1)
+             for s in (slice(0, cut), slice(cut, T))]
+    torch.cuda.synchronize()
+    assert torch.equal(A, torch.cat(parts, dim=1)), f"pipelined A (ragged tail) differs from the one-tile kernel, K={K}"
 
 
 @pytest.mark.parametrize("B,T,H,K,V,seed", [(1, 64, 2, 64, 64, 4242), (2, 128, 4, 64, 64, 5236),
