@@ -141,6 +141,25 @@ std::vector<Pattern> patterns() {
   for (int q : {0, 8})
     add(ps, "ds_read_b128 16 rows, row pairs at one chunk, q " + std::to_string(q), kR16,
         [&](int l) { return (uint32_t)(4096 + (l & 15) * 256 + (((q + (l >> 4)) ^ (l & 14)) << 4)); });
+  // Minimal pairs (ds_read_b128): every lane of pass 0 but lane 1 reads one
+  // base address (a broadcast), lanes 16-63 read a contiguous run elsewhere;
+  // lane 1 reads (block, chunk) at 256 bytes per block, 16 bytes per chunk.
+  add(ps, "b128 broadcast, all 64 lanes one address", kR16, [](int) { return 0; });
+  add(ps, "b128 broadcast pass 0, rest contiguous", kR16, [](int l) { return l < 16 ? 0 : 0x8000 + (l - 16) * 16; });
+  const int pairs[][4] = {{0, 0, 1, 0},  {0, 0, 2, 0},  {0, 0, 3, 0},  {0, 0, 4, 0},  {0, 0, 8, 0},
+                          {0, 0, 9, 0},  {0, 0, 16, 0}, {0, 0, 17, 0}, {0, 0, 32, 0}, {0, 0, 1, 15},
+                          {0, 0, 1, 1},  {0, 0, 1, 14}, {0, 0, 2, 1},  {0, 0, 3, 15}, {0, 0, 0, 1},
+                          {16, 0, 17, 0}, {16, 0, 18, 0}, {16, 0, 24, 0}, {16, 0, 25, 0}, {16, 0, 17, 15},
+                          {16, 0, 17, 1}, {1, 0, 3, 0},  {1, 0, 2, 0},  {0, 1, 1, 0},  {8, 0, 9, 0}};
+  for (const auto& q : pairs) {
+    const int b0 = q[0], c0 = q[1], b1 = q[2], c1 = q[3];
+    add(ps, "b128 pair (" + std::to_string(b0) + "," + std::to_string(c0) + ") vs (" + std::to_string(b1) + "," +
+                std::to_string(c1) + ")",
+        kR16, [=](int l) {
+          if (l >= 16) return 0x8000 + (l - 16) * 16;
+          return l == 1 ? b1 * 256 + c1 * 16 : b0 * 256 + c0 * 16;
+        });
+  }
   return ps;
 }
 
